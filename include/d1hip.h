@@ -1,0 +1,110 @@
+/* d1hip — MI355X-native batched DCSS D:1 environment (C ABI).
+ *
+ * One call steps a batch of independent D:1 worlds on the GPU: the player's
+ * semantic action (MOVE 0-7, ATTACK 8-15, WAIT 16, REST 17, DESCEND 18),
+ * field-of-view reveal, LOS-gated monster waking, the monster turn loop
+ * (energy scheduler, greedy pathing on a distance-from-player field, melee),
+ * terminal checks with in-step auto-reset, the 15x15x8 uint8 egocentric
+ * observation and a per-env 32-bit state hash.
+ *
+ * The entry points mirror the reference's `learn_*` C ABI
+ * (gpu-d1/src/learn.cu:643-675, gpu-d1/branches/d1-stairs-v2/src/learn.cu:912-945):
+ * size queries, init, step, step-with-active-mask. Differences, by design:
+ *   - observations are uint8 [n, 15, 15, 8] (channel-last) instead of fp32 vectors;
+ *   - the per-env state row also holds that env's level (floor + spawnable cells),
+ *     so each env may carry its own generated level;
+ *   - a 32-bit state hash per env is written on every call;
+ *   - only the GPU path exists here (the reference's `gpu` flag selected a host
+ *     loop; the CPU restatement used for verification lives outside this library).
+ *
+ * All pointers are device pointers except `cfg` and `tab`, which are host structs
+ * copied by value into the launch. Calls are asynchronous on `stream` (a
+ * hipStream_t; 0 = the null stream). Return value: 0 on success, a hipError_t
+ * code for launch failures, or a negative D1_E* code for rejected arguments.
+ * The library allocates no memory and keeps no global state.
+ */
+#ifndef D1HIP_H
+#define D1HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define D1_W 80
+#define D1_H 70
+#define D1_N 5600
+#define D1_VIEW 15                    /* 15x15 window, radius 7 */
+#define D1_OBS_CH 8                   /* wall, floor, visible, monster kind+1, monster hp, player hp, stairs, frontier */
+#define D1_OBS_BYTES (D1_VIEW * D1_VIEW * D1_OBS_CH)   /* 1800 */
+#define D1_ACTIONS 19
+#define D1_OUT 8                      /* reward, done, clear, killed, hp, ticks, death, timeout (gpu-d1/src/learn.cu:590-592) */
+#define D1_MAX_MONSTERS 64
+
+#define D1_E_ARG (-1)                 /* null pointer, bad size or bad mode */
+#define D1_E_CONFIG (-2)              /* config outside the supported ranges */
+
+/* Monster kind: speed, damage, to-hit, shield bypass (gpu-d1/src/sim.h:61-63). */
+typedef struct D1Kind { int32_t speed, damage, tohit, bypass; } D1Kind;
+
+/* Runtime rules. The first block is the reference's sim::Config minus its
+ * `player` position (gpu-d1/src/sim.h:64-67, packed by gpu-d1/scripts/learn_env.py:67-71);
+ * the rest are the task switches that the reference selects with -D flags
+ * (gpu-d1/Makefile:14-95, gpu-d1/branches/d1-stairs-v2/scripts/assets.py:5). */
+typedef struct D1Config {
+    int32_t count;            /* monsters per world, 1..max_monsters of the state layout */
+    int32_t hp, ac100, ev100, sh100, shield_limit, regen, repair;
+    int32_t gdr[2];           /* floor((65536*(ac+j))^(1/4)) for the two AC roundings */
+    D1Kind kinds[6];
+    int32_t limit;            /* deadline in physical turns */
+    int32_t rng_mode;         /* 0: PCG32 per env (reference stream), 1: Philox4x32-10 counter RNG */
+    int32_t level_mode;       /* 0: one shared map from D1Tables, 1: generated level per env */
+    int32_t roster_mode;      /* 0: kind i%6 and HP {8,10,12,16,12,10}[i%6]; 1: kind U{0..5}, HP U[hp_lo,hp_hi] */
+    int32_t hp_lo, hp_hi;
+    int32_t awake_pct;        /* monsters awake at spawn: 0 none, 100 all (no draw), else U{0..99} < pct */
+    int32_t wake_los;         /* 1: waking needs the monster's LOS to the player, 0: Chebyshev <= 6 only */
+    int32_t stairs;           /* 0 or 3 stairs placed per episode */
+    int32_t clear_on_kill_all;/* 1: killing every monster also clears the level */
+    int32_t explore_milli, kill_milli, clear_milli, death_milli, step_milli;
+    float turn_cost;          /* subtracted per physical turn after the milli sum */
+} D1Config;
+
+/* Static tables. `floor`/`cells` are used when level_mode == 0 (byte per cell,
+ * row-major, cells = spawnable floor in increasing cell order); `ray_slots` is the
+ * [11][64] uint64 per-target LOS ray table (blocker bit j = y*8+x of the +x/+y
+ * quadrant), always required. */
+typedef struct D1Tables {
+    const uint8_t *floor;
+    const uint8_t *cells;
+    const uint64_t *ray_slots;
+    int32_t nslots;           /* 11 for the native ray export */
+} D1Tables;
+
+/* Bytes per env of the state row for a given monster capacity (8, 16, 40 or 64). */
+int d1_state_bytes(int max_monsters);
+int d1_obs_bytes(void);
+int d1_action_size(void);
+int d1_out_size(void);
+int d1_config_bytes(void);
+
+/* Replaces learn_init (gpu-d1/src/learn.cu:649-660): seeds env i's RNG
+ * (PCG: seed(mix(seed+i), i+1); counter: key=seed, env=i), builds or copies its
+ * level, runs the episode reset and writes the first observation and hash.
+ * `state` is uint8 [n, d1_state_bytes(max_monsters)]. */
+int d1_init(void *state, int n, int max_monsters, const D1Config *cfg, const D1Tables *tab,
+            uint64_t seed, uint8_t *obs, uint32_t *hash, void *stream);
+
+/* Replaces learn_step / learn_step_active (gpu-d1/src/learn.cu:661-670,
+ * gpu-d1/branches/d1-stairs-v2/src/learn.cu:853-875): one joint action per env
+ * (int64, as the reference's trainer passes them), then the observation of the
+ * post-step (post-reset when done) state. `out` is float [n, D1_OUT].
+ * `active` may be null; an inactive env keeps its state and all its output
+ * rows untouched and consumes no RNG (gpu-d1/scripts/test_fast_frontier.py:89-100). */
+int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1Tables *tab,
+            const int64_t *actions, uint8_t *obs, float *out, uint32_t *hash,
+            const uint8_t *active, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

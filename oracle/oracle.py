@@ -1,0 +1,113 @@
+"""TEST INFRASTRUCTURE ONLY — ctypes wrapper of the CPU restatement (libd1oracle.so).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this.
+"""
+import ctypes as C
+import importlib
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+pkg = importlib.import_module('dcss-auto_amd')
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = HERE / 'libd1oracle.so'
+        if not path.exists():
+            raise RuntimeError(f'{path} is not built; run __graft_entry__.build()')
+        L = C.CDLL(str(path))
+        p, i = C.c_void_p, C.c_int
+        L.o_mix.restype = C.c_uint64
+        L.o_mix.argtypes = [C.c_uint64]
+        L.o_philox.argtypes = [p, p, p]
+        L.o_set_rays.argtypes = [i, p, p]
+        L.o_los_bitset.argtypes = [p, i, p]
+        L.o_los.argtypes = [p, i, i, i]
+        L.o_level_generate.argtypes = [C.c_uint64, C.c_uint32, p]
+        L.o_init.argtypes = [p, i, p, p, p, C.c_uint64, p, p, i]
+        L.o_step.argtypes = [p, i, p, p, p, p, p, p, i]
+        L.o_obs.argtypes = [p, p, p]
+        L.o_hash.restype = C.c_uint32
+        L.o_hash.argtypes = [p, p]
+        L.o_heuristic.argtypes = [p, p]
+        L.o_rng_ops.argtypes = [i, C.c_uint64, C.c_uint64, i, p, p, p, p]
+        L.o_wait_run.argtypes = [i, i, i, i, C.c_uint64, C.c_uint32, p, p, p, p, p, C.c_int32, p]
+        r = pkg.data.rays()
+        ends = np.ascontiguousarray(r['ends'], np.int8)
+        masks = np.ascontiguousarray(r['masks'], np.uint64)
+        L.o_set_rays(len(masks), ends.ctypes.data, masks.ctypes.data)
+        _LIB = L
+    return _LIB
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class OracleEnv:
+    """Batch of worlds stepped by the CPU restatement; numpy buffers mirror the GPU Env."""
+
+    def __init__(self, batch, cfg, seed=0, threads=1):
+        self.L, self.batch, self.cfg, self.threads = lib(), batch, cfg, threads
+        self.state = np.zeros((batch, self.L.o_state_bytes()), np.uint8)
+        self.obs = np.zeros((batch, 15, 15, 8), np.uint8)
+        self.out = np.zeros((batch, 8), np.float32)
+        self.hash = np.zeros(batch, np.uint32)
+        self.floor, self.cells = pkg.shared_map_arrays()
+        self.reset(seed)
+
+    def reset(self, seed):
+        self.L.o_init(ptr(self.state), self.batch, C.byref(self.cfg), ptr(self.floor), ptr(self.cells),
+                      seed, ptr(self.obs), ptr(self.hash), self.threads)
+        return self.obs
+
+    def step(self, actions, active=None):
+        a = np.ascontiguousarray(actions, np.int64)
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        self.L.o_step(ptr(self.state), self.batch, C.byref(self.cfg), ptr(a), ptr(self.obs), ptr(self.out),
+                      ptr(self.hash), ptr(act), self.threads)
+        return self.obs, self.out
+
+    def heuristic(self):
+        n = self.state.shape[1]
+        return np.array([self.L.o_heuristic(self.state[i:].ctypes.data, C.byref(self.cfg)) for i in range(self.batch)],
+                        np.int64) if n else None
+
+    # canonical fields (OState layout in oracle/d1_oracle.h)
+    def fields(self):
+        dt = np.dtype([('rng_state', '<u8'), ('rng_inc', '<u8'), ('key0', '<u4'), ('key1', '<u4'), ('rt', '<u4'),
+                       ('renv', '<u4'), ('domain', '<u4'), ('k', '<u4'), ('mode', '<i4'), ('pad', '<i4'),
+                       ('env_id', '<u4'), ('t', '<u4'), ('episode', '<i4'), ('player', '<i4'), ('hp', '<i4'),
+                       ('regen', '<i4'), ('blocks', '<i4'), ('ticks', '<i4'), ('killed', '<i4'),
+                       ('decisions', '<i4'), ('floor_seen', '<i4'), ('first_stair_tick', '<i4'),
+                       ('stairs', '<i4', 3), ('ncells', '<i4'), ('vis_origin', '<i4'), ('vis', '<u4', 10), ('pos', '<i2', 64), ('mhp', '<i2', 64),
+                       ('energy', '<i2', 64), ('awake', 'u1', 64), ('kind', 'u1', 64), ('occ', '<i2', 5600),
+                       ('viewed', 'u1', 5600), ('floor', 'u1', 5600), ('cells', '<i2', 5600)])
+        assert dt.itemsize <= self.state.shape[1]
+        return np.frombuffer(self.state.tobytes(), dtype=np.dtype({'names': dt.names, 'formats': [dt.fields[n][0] for n in dt.names],
+                                                                  'offsets': [dt.fields[n][1] for n in dt.names],
+                                                                  'itemsize': self.state.shape[1]}))
+
+
+def level(seed, env):
+    f = np.zeros(5600, np.uint8)
+    lib().o_level_generate(seed, env, f.ctypes.data)
+    return f
+
+
+def los_bitset(floor, origin):
+    out = np.zeros(10, np.uint32)
+    lib().o_los_bitset(np.ascontiguousarray(floor, np.uint8).ctypes.data, origin, out.ctypes.data)
+    return out
+
+
+def philox(ctr, key):
+    c = np.array(ctr, np.uint32)
+    k = np.array(key, np.uint32)
+    o = np.zeros(4, np.uint32)
+    lib().o_philox(c.ctypes.data, k.ctypes.data, o.ctypes.data)
+    return o
