@@ -1,0 +1,34 @@
+"""Loads libd1hip.so (built in-tree by build.py) and declares its C ABI (include/d1hip.h).
+
+There is no fallback: without the built library every entry point raises."""
+import ctypes as C
+import pathlib
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / 'libd1hip.so'
+_LIB = None
+
+SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
+           'd1_init', 'd1_step')
+
+
+def load():
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f'{LIB_PATH} is missing: build it with __graft_entry__.build() '
+                               '(the D:1 environment has no CPU fallback)')
+        L = C.CDLL(str(LIB_PATH))
+        p, i = C.c_void_p, C.c_int
+        L.d1_state_bytes.argtypes = [i]
+        for name in ('d1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes'):
+            getattr(L, name).argtypes = []
+        L.d1_init.argtypes = [p, i, i, p, p, C.c_uint64, p, p, p]
+        L.d1_step.argtypes = [p, i, i, p, p, p, p, p, p, p, p]
+        _LIB = L
+    return _LIB
+
+
+def check(code, what):
+    if code:
+        raise RuntimeError(f'{what} failed with code {code}')

@@ -194,27 +194,34 @@ int o_los(const uint8_t *floor, int origin, int target, int radius) {
 }
 
 /* ------------------------------------------------------------------ level generator */
-/* Build-owned spec (the reference loads native Crawl exports instead): 6-9
- * rectangular rooms placed by rejection on an 80x70 grid with a one-cell wall gap,
- * then an L-shaped corridor between consecutive room centres (orientation by
- * one draw), so every floor cell is connected. Counter stream (seed, env, t=0,
- * domain 1). Room: w 4-12, h 3-8, x in [1, W-w-1], y in [1, H-h-1]; at most
- * 4096 placement attempts. */
+/* Build-owned spec (the reference loads native Crawl exports instead). The
+ * interior is split into 3x3 sectors of 26x22 cells (x0 = 1+26c, y0 = 1+22r);
+ * n = 6 + U{0..3} sectors are chosen by a partial Fisher-Yates shuffle of 0..8
+ * (swap i with i + U{0..8-i}); in shuffle order each chosen sector gets one room,
+ * w = 4 + U{0..8}, h = 3 + U{0..5}, x = x0 + U{0..26-w}, y = y0 + U{0..22-h}; then
+ * consecutive rooms are joined by an L-shaped corridor between their centres
+ * (x + w/2, y + h/2), vertical leg first when a draw U{0,1} is 1. Every level is
+ * connected, never touches the border, and has at least 72 floor cells. Counter
+ * stream (seed, env, t=0, domain 1); the draw count is fixed by n. */
 void o_level_generate(uint64_t seed, uint32_t env, uint8_t *floor) {
     ORng g;
     ctr_stream(&g, seed, env, 0, 1);
     memset(floor, 0, N);
-    int target = 6 + rng_r(&g, 4);
-    int rx[9], ry[9], rw[9], rh[9], n = 0;
-    for (int attempt = 0; attempt < 4096 && n < target; attempt++) {
+    int n = 6 + rng_r(&g, 4);
+    int order[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
+    for (int i = 0; i < n; i++) {
+        int j = i + rng_r(&g, 9 - i), tmp = order[i];
+        order[i] = order[j];
+        order[j] = tmp;
+    }
+    int rx[9], ry[9], rw[9], rh[9];
+    for (int i = 0; i < n; i++) {
+        int x0 = 1 + 26 * (order[i] % 3), y0 = 1 + 22 * (order[i] / 3);
         int w = 4 + rng_r(&g, 9), h = 3 + rng_r(&g, 6);
-        int x = 1 + rng_r(&g, W - w - 1), y = 1 + rng_r(&g, H - h - 1);
-        int ok = 1;
-        for (int j = 0; j < n; j++)
-            if (!(x + w + 1 <= rx[j] || rx[j] + rw[j] + 1 <= x || y + h + 1 <= ry[j] ||
-                  ry[j] + rh[j] + 1 <= y)) ok = 0;
-        if (!ok) continue;
-        rx[n] = x; ry[n] = y; rw[n] = w; rh[n] = h; n++;
+        rx[i] = x0 + rng_r(&g, 27 - w);
+        ry[i] = y0 + rng_r(&g, 23 - h);
+        rw[i] = w;
+        rh[i] = h;
     }
     for (int j = 0; j < n; j++)
         for (int y = ry[j]; y < ry[j] + rh[j]; y++)
@@ -288,8 +295,12 @@ static void reset(OState *s, const D1Config *c) {
     s->hp = c->hp; s->regen = 0; s->blocks = 0;
     s->ticks = 0; s->decisions = 0; s->killed = 0; s->floor_seen = 0;
     for (int i = 0; i < c->count; i++) {
-        int p;
-        do { p = s->cells[rng_r(g, s->ncells)]; } while (p == s->player || s->occ[p] >= 0);
+        int p, tries = 0;
+        do { p = s->cells[rng_r(g, s->ncells)]; } while ((p == s->player || s->occ[p] >= 0) && ++tries < 65536);
+        /* The reference retries without bound; the cap (never reached with >= 72 cells
+         * and <= 64 monsters) bounds the GPU loop, falling back to the first free cell. */
+        if (p == s->player || s->occ[p] >= 0)
+            for (int j = 0; j < s->ncells; j++) { p = s->cells[j]; if (p != s->player && s->occ[p] < 0) break; }
         s->pos[i] = (int16_t)p;
         s->occ[p] = (int16_t)i;
         if (c->roster_mode == 0) { s->kind[i] = (uint8_t)(i % 6); s->mhp[i] = (int16_t)MHP[i % 6]; }

@@ -1,0 +1,62 @@
+"""HIP environment vs the CPU oracle: per-step state hash, out[] and the uint8
+observation must be identical (integer/byte work is bit-exact; reward floats too)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # name, config factory args, batch, steps, actions
+    ('baseline8', ('baseline_config', 8), 64, 300, 16),
+    ('reference24', ('reference_config', 24), 40, 300, 19),
+    ('v1_8', ('v1_config', 8), 37, 300, 9),
+    ('stress40', ('stress_config',), 24, 200, 16),
+]
+
+
+def make(pkg, spec):
+    fn = getattr(pkg, spec[0])
+    return fn(*spec[1:])
+
+
+def compare(gpu, cpu, step, name):
+    torch.cuda.synchronize()
+    gh = gpu.hash.cpu().numpy().view(np.uint32)
+    bad = np.flatnonzero(gh != cpu.hash)
+    go = gpu.obs.cpu().numpy()
+    bad_obs = np.flatnonzero((go != cpu.obs).reshape(len(go), -1).any(1))
+    gout = gpu.out.cpu().numpy()
+    bad_out = np.flatnonzero((gout.view(np.uint32) != cpu.out.view(np.uint32)).any(1)) if step >= 0 else []
+    if len(bad) or len(bad_obs) or len(bad_out):
+        e = int((list(bad) + list(bad_obs) + list(bad_out))[0])
+        f = cpu.fields()[e]
+        msg = (f'{name} step {step}: {len(bad)} hash, {len(bad_obs)} obs, {len(bad_out)} out mismatches; env {e} '
+               f'player {f["player"]} hp {f["hp"]} ticks {f["ticks"]} episode {f["episode"]} '
+               f'out gpu {gout[e]} cpu {cpu.out[e]}')
+        if e in bad_obs:
+            d = np.argwhere(go[e] != cpu.obs[e])[:5]
+            msg += f' obs diffs (dy,dx,ch) {d.tolist()} gpu {[int(go[e][tuple(i)]) for i in d]} ' \
+                   f'cpu {[int(cpu.obs[e][tuple(i)]) for i in d]}'
+        pytest.fail(msg)
+
+
+@pytest.mark.parametrize('name,spec,batch,steps,nact', CASES)
+def test_hip_matches_oracle(pkg, name, spec, batch, steps, nact):
+    print(f'[parity] {name} batch={batch} steps={steps}', flush=True)
+    cfg = make(pkg, spec)
+    gpu = pkg.Env(batch, cfg, seed=91)
+    cpu = O.OracleEnv(batch, cfg, seed=91, threads=8)
+    compare(gpu, cpu, -1, name)
+    rng = np.random.default_rng(137)
+    dones = 0
+    for k in range(steps):
+        a = rng.integers(0, nact, batch).astype(np.int64) if k % 2 else cpu.heuristic()
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, name)
+        dones += int(cpu.out[:, 1].sum())
+    assert dones > 0
+    print(f'[parity] {name} ok, {dones} episode ends', flush=True)
