@@ -1,0 +1,130 @@
+#!/usr/bin/env python3
+"""Benchmark of the D:1 rollout hot path on one MI355X.
+
+One step = one pass over 65,536 worlds: the HIP env step (transition + auto-reset +
+15x15x8 uint8 observation + state hash), the bf16 policy MLP 1800->256->256 with a
+16-logit head and a value head (hipBLASLt via torch), and the counter-RNG categorical
+sampler (HIP) that produces the next actions. Inputs stay resident in HBM; the timed
+region is bracketed by synchronisations. Prints one JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--envs N] [--gpus 1]
+"""
+import argparse
+import importlib
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+# Algorithmic bytes per env step at 8 monsters: obs 1800 +
+# action 1 + reward/done/hash 9 + 2 x (24 + 7 x 8) dynamic state + 600 seen/viewed band
+# + 700 level bitmap.
+STEP_BYTES = {8: 3270, 40: 3718}
+TRUNK_FLOPS = 2 * (1800 * 256 + 256 * 256 + 256 * 17)
+
+
+def cpu_baseline(envs=1024, steps=1000, threads=None):
+    """The CPU restatement (oracle/, OpenMP over worlds) on config C1: 1,024 generated
+    levels, 8 monsters, uniform random actions over 16, 1,000 steps."""
+    import numpy as np
+    from oracle import oracle as O
+    pkg = importlib.import_module('dcss-auto_amd')
+    threads = threads or min(16, os.cpu_count() or 1)
+    env = O.OracleEnv(envs, pkg.baseline_config(), seed=1, threads=threads)
+    actions = np.random.default_rng(2).integers(0, 16, (steps, envs)).astype(np.int64)
+    t0 = time.perf_counter()
+    for k in range(steps):
+        env.step(actions[k])
+    dt = time.perf_counter() - t0
+    return {'value': envs * steps / dt, 'unit': 'env decisions/s', 'cores': threads, 'kind': 'port',
+            'sample': f'C1 full: {envs} generated levels x {steps} steps, 8 monsters, random actions, '
+                      f'step+obs+hash, {dt:.2f} s wall'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=128)
+    ap.add_argument('--warmup', type=int, default=8)
+    ap.add_argument('--envs', type=int, default=65536)
+    ap.add_argument('--monsters', type=int, default=8)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
+        print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = importlib.import_module('dcss-auto_amd')
+    policy_mod = importlib.import_module('dcss-auto_amd.policy')
+    dev = torch.device('cuda:0')
+    cfg = pkg.baseline_config(args.monsters) if args.monsters <= 8 else pkg.stress_config()
+    n = args.envs
+    env = pkg.Env(n, cfg, seed=1)
+    model = policy_mod.Policy(seed=0).to(dev).to(torch.bfloat16)
+    actions = torch.zeros(n, dtype=torch.int64, device=dev)
+    logp = torch.zeros(n, dtype=torch.float32, device=dev)
+    seed = 12345
+
+    def one_step(t, ev=None):
+        if ev is not None:
+            ev[0].record()
+        env.step(actions)
+        if ev is not None:
+            ev[1].record()
+        with torch.no_grad():
+            logits, value = model(env.obs)
+        if ev is not None:
+            ev[2].record()
+        policy_mod.sample(logits, seed, t, actions, logp)
+
+    for t in range(args.warmup):
+        one_step(t)
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        one_step(args.warmup + k, events[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    trunk_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    decisions = n * args.steps / wall
+    step_bytes = STEP_BYTES.get(args.monsters, 3270)
+    achieved = step_bytes * n / (step_ms * 1e-3) / 1e9
+    trunk_tflops = TRUNK_FLOPS * n / (trunk_ms * 1e-3) / 1e12
+    result = {
+        'metric': 'env decisions/sec at 65,536 envs (1 GPU): step+obs+policy+sample',
+        'value': decisions,
+        'unit': 'decisions/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': wall / args.steps * 1e3,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'int16/u8 env, bf16 trunk',
+        'data': 'synthetic: generated 80x70 levels, random-init N(0,0.02) bf16 policy',
+        'config': {'workload': 'C3', 'envs': n, 'monsters': args.monsters, 'obs': '15x15x8 uint8',
+                   'policy': '1800-256-256 ReLU, 16 logits + value, bf16', 'sampler': 'Philox counter RNG',
+                   'rollout_steps': args.steps},
+        'roofline': {'bound': 'hbm', 'kernel': 'd1::k_step', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': None,
+                     'bytes_per_env_step': step_bytes, 'avg_launch_ms': step_ms},
+        'trunk': {'bound': 'mfma', 'achieved': trunk_tflops, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                  'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms},
+    }
+    if not args.no_cpu_baseline:
+        result['cpu_baseline'] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

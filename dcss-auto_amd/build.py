@@ -3,7 +3,7 @@ import pathlib
 import subprocess
 
 HERE = pathlib.Path(__file__).resolve().parent
-SOURCES = [HERE / 'csrc' / 'd1_env.hip']
+SOURCES = [HERE / 'csrc' / 'd1_env.hip', HERE / 'csrc' / 'd1_policy.hip']
 FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared', '-ffp-contract=off',
          '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops']
 

@@ -104,6 +104,23 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
             const int64_t *actions, uint8_t *obs, float *out, uint32_t *hash,
             const uint8_t *active, void *stream);
 
+/* Categorical sampling with the counter RNG; replaces torch.distributions.Categorical
+ * sample/log_prob in the rollout (gpu-d1/scripts/run_ring_ablations.py:350-351).
+ * logits: float [n, k] (row stride `ld` floats), 1 <= k <= 64. For env i the uniform
+ * is u = (w >> 8) * 2^-24 with w = word 0 of Philox4x32-10(ctr={0, t, i, 3}, key=seed);
+ * the action is the first j with u < cumsum_j(softmax(logits)) (fp32, left to right),
+ * else k-1. Writes int64 actions and fp32 log-probabilities (either may be null). */
+int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t t,
+              int64_t *actions, float *logp, void *stream);
+
+/* Reverse-time GAE over a [T, n] rollout (gpu-d1/scripts/run_ring_ablations.py:354-360):
+ *   live = 1 - done[t]; delta = reward[t] + (gamma*next)*live - value[t];
+ *   gae = delta + (gamma_lambda*live)*gae; adv[t] = gae; next = value[t]
+ * with next = bootstrap for t = T-1 and every product rounded separately (fp32).
+ * `done` is uint8 [T, n]; returns[t] = adv[t] + value[t]. */
+int d1_gae(const float *reward, const uint8_t *done, const float *value, const float *bootstrap,
+           int T, int n, float gamma, float gamma_lambda, float *adv, float *returns, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
