@@ -29,6 +29,18 @@ STEP_BYTES = {8: 3270, 40: 3718}
 TRUNK_FLOPS = 2 * (1800 * 256 + 256 * 256 + 256 * 17)
 
 
+def measured_traffic(path=ROOT / 'profiles' / 'k_step_hbm_traffic.md'):
+    """HBM bytes per k_step launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (calibrated against a copy kernel), or None when absent."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith('traffic_bytes_per_launch:'):
+                return float(line.split(':')[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(envs=1024, steps=1000, threads=None):
     """The CPU restatement (oracle/, OpenMP over worlds) on config C1: 1,024 generated
     levels, 8 monsters, uniform random actions over 16, 1,000 steps."""
@@ -55,6 +67,8 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--mode', choices=['rollout', 'counters'], default='rollout',
+                    help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
@@ -71,6 +85,17 @@ def main():
     actions = torch.zeros(n, dtype=torch.int64, device=dev)
     logp = torch.zeros(n, dtype=torch.float32, device=dev)
     seed = 12345
+    if args.mode == 'counters':
+        src = torch.ones(64 << 20, dtype=torch.int32, device=dev)   # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        for t in range(args.steps):
+            actions.random_(0, 16)
+            env.step(actions)
+        torch.cuda.synchronize()
+        print(json.dumps({'mode': 'counters', 'copy_bytes': src.numel() * 4, 'env_steps': args.steps, 'envs': n}))
+        return
 
     def one_step(t, ev=None):
         if ev is not None:
@@ -116,7 +141,7 @@ def main():
                    'policy': '1800-256-256 ReLU, 16 logits + value, bf16', 'sampler': 'Philox counter RNG',
                    'rollout_steps': args.steps},
         'roofline': {'bound': 'hbm', 'kernel': 'd1::k_step', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': None,
+                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': measured_traffic(),
                      'bytes_per_env_step': step_bytes, 'avg_launch_ms': step_ms},
         'trunk': {'bound': 'mfma', 'achieved': trunk_tflops, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                   'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms},

@@ -64,63 +64,62 @@ struct Smem {
 };
 
 // ---------------------------------------------------------------- small helpers
-__device__ inline int lane_id() { return (int)threadIdx.x; }
-__device__ inline int imin(int a, int b) { return a < b ? a : b; }
-__device__ inline int imax(int a, int b) { return a > b ? a : b; }
-__device__ inline int iabs(int a) { return a < 0 ? -a : a; }
-__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ inline int lane_val(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
-__device__ inline uint64_t ballot(bool b) { return __ballot(b); }
-__device__ inline int wave_max(int v) {
+__device__ __forceinline__ int lane_id() { return (int)threadIdx.x; }
+__device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+__device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
+__device__ __forceinline__ int iabs(int a) { return a < 0 ? -a : a; }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int lane_val(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
+__device__ __forceinline__ int wave_max(int v) {
     for (int o = 32; o; o >>= 1) v = imax(v, __shfl_xor(v, o));
     return uni(v);
 }
-__device__ inline uint32_t wave_sum(uint32_t v) {
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
     for (int o = 32; o; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
     return (uint32_t)uni((int)v);
 }
 // gpu-d1/src/sim.h:14
-__device__ inline int cheb(int a, int b) { return imax(iabs(a % W - b % W), iabs(a / W - b / W)); }
+__device__ __forceinline__ int cheb(int a, int b) { return imax(iabs(a % W - b % W), iabs(a / W - b / W)); }
 // gpu-d1/src/sim.h:201-206: N, E, S, W, NE, SE, SW, NW
-__device__ inline int nbr(int p, int d) {
+__device__ __forceinline__ int nbr(int p, int d) {
     int ddx = d == 1 || d == 4 || d == 5 ? 1 : d == 3 || d == 6 || d == 7 ? -1 : 0;
     int ddy = d == 0 || d == 4 || d == 7 ? -1 : d == 2 || d == 5 || d == 6 ? 1 : 0;
     int x = p % W + ddx, y = p / W + ddy;
     return x >= 0 && x < W && y >= 0 && y < H ? y * W + x : -1;
 }
-__device__ inline bool inb(int x, int y) { return x >= 0 && x < W && y >= 0 && y < H; }
-__device__ inline bool bit_at(const uint32_t *bm, int x, int y) {
+__device__ __forceinline__ bool inb(int x, int y) { return x >= 0 && x < W && y >= 0 && y < H; }
+__device__ __forceinline__ bool bit_at(const uint32_t *bm, int x, int y) {
     return (bm[y * RW + (x >> 5)] >> (x & 31)) & 1u;
 }
-__device__ inline bool bit(const uint32_t *bm, int p) { return bit_at(bm, p % W, p / W); }
+__device__ __forceinline__ bool bit(const uint32_t *bm, int p) { return bit_at(bm, p % W, p / W); }
 
 struct Row {
     uint32_t a, b, c;   // bits 0-31, 32-63, 64-79
 };
-__device__ inline Row row_ld(const uint32_t *bm, int y) { return {bm[y * RW], bm[y * RW + 1], bm[y * RW + 2]}; }
-__device__ inline void row_st(uint32_t *bm, int y, Row r) { bm[y * RW] = r.a; bm[y * RW + 1] = r.b; bm[y * RW + 2] = r.c; }
-__device__ inline Row row_or(Row x, Row y) { return {x.a | y.a, x.b | y.b, x.c | y.c}; }
-__device__ inline Row row_and(Row x, Row y) { return {x.a & y.a, x.b & y.b, x.c & y.c}; }
-__device__ inline Row row_andn(Row x, Row y) { return {x.a & ~y.a, x.b & ~y.b, x.c & ~y.c}; }
-__device__ inline Row row_shl1(Row r) { return {r.a << 1, (r.b << 1) | (r.a >> 31), ((r.c << 1) | (r.b >> 31)) & 0xFFFFu}; }
-__device__ inline Row row_shr1(Row r) { return {(r.a >> 1) | (r.b << 31), (r.b >> 1) | (r.c << 31), r.c >> 1}; }
-__device__ inline bool row_any(Row r) { return (r.a | r.b | r.c) != 0; }
-__device__ inline int row_popc(Row r) { return __popc(r.a) + __popc(r.b) + __popc(r.c); }
+__device__ __forceinline__ Row row_ld(const uint32_t *bm, int y) { return {bm[y * RW], bm[y * RW + 1], bm[y * RW + 2]}; }
+__device__ __forceinline__ void row_st(uint32_t *bm, int y, Row r) { bm[y * RW] = r.a; bm[y * RW + 1] = r.b; bm[y * RW + 2] = r.c; }
+__device__ __forceinline__ Row row_or(Row x, Row y) { return {x.a | y.a, x.b | y.b, x.c | y.c}; }
+__device__ __forceinline__ Row row_and(Row x, Row y) { return {x.a & y.a, x.b & y.b, x.c & y.c}; }
+__device__ __forceinline__ Row row_andn(Row x, Row y) { return {x.a & ~y.a, x.b & ~y.b, x.c & ~y.c}; }
+__device__ __forceinline__ Row row_shl1(Row r) { return {r.a << 1, (r.b << 1) | (r.a >> 31), ((r.c << 1) | (r.b >> 31)) & 0xFFFFu}; }
+__device__ __forceinline__ Row row_shr1(Row r) { return {(r.a >> 1) | (r.b << 31), (r.b >> 1) | (r.c << 31), r.c >> 1}; }
+__device__ __forceinline__ bool row_any(Row r) { return (r.a | r.b | r.c) != 0; }
+__device__ __forceinline__ int row_popc(Row r) { return __popc(r.a) + __popc(r.b) + __popc(r.c); }
+// bits [x0, x1] of the 32-bit word starting at bit `base`
+__device__ __forceinline__ uint32_t word_range(int x0, int x1, int base) {
+    int lo = imax(x0 - base, 0), hi = imin(x1 - base, 31);
+    return lo > hi ? 0u : ((hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u)) & ~((1u << lo) - 1u));
+}
 // bits [x0, x1] (inclusive, clipped to 0..79)
-__device__ inline Row row_range(int x0, int x1) {
+__device__ __forceinline__ Row row_range(int x0, int x1) {
     x0 = imax(x0, 0);
     x1 = imin(x1, W - 1);
-    Row r{0, 0, 0};
-    if (x0 > x1) return r;
-    uint32_t w[3];
-    for (int k = 0; k < 3; k++) {
-        int lo = imax(x0 - 32 * k, 0), hi = imin(x1 - 32 * k, 31);
-        w[k] = lo > hi ? 0u : ((hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u)) & ~((1u << lo) - 1u));
-    }
-    return {w[0], w[1], w[2] & 0xFFFFu};
+    if (x0 > x1) return Row{0, 0, 0};
+    return Row{word_range(x0, x1, 0), word_range(x0, x1, 32), word_range(x0, x1, 64) & 0xFFFFu};
 }
 // 15-bit window pattern v (bit k = x px-7+k) placed on an 80-bit row
-__device__ inline Row row_place15(uint32_t v, int px) {
+__device__ __forceinline__ Row row_place15(uint32_t v, int px) {
     int shift = px - 7;
     uint64_t lo, hi;
     if (shift < 0) { lo = (uint64_t)v >> (-shift); hi = 0; }
@@ -129,7 +128,7 @@ __device__ inline Row row_place15(uint32_t v, int px) {
     return {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi & 0xFFFFu};
 }
 // position of the j-th set bit (j < popc(v))
-__device__ inline int select32(uint32_t v, int j) {
+__device__ __forceinline__ int select32(uint32_t v, int j) {
     int pos = 0;
     for (int s = 16; s; s >>= 1) {
         int c = __popc(v & ((1u << s) - 1u));
@@ -137,7 +136,7 @@ __device__ inline int select32(uint32_t v, int j) {
     }
     return pos;
 }
-__device__ inline int row_select(Row r, int j) {
+__device__ __forceinline__ int row_select(Row r, int j) {
     int c0 = __popc(r.a);
     if (j < c0) return select32(r.a, j);
     j -= c0;
@@ -145,12 +144,12 @@ __device__ inline int row_select(Row r, int j) {
     if (j < c1) return 32 + select32(r.b, j);
     return 64 + select32(r.c, j - c1);
 }
-__device__ inline uint32_t fmix32(uint32_t h) {
+__device__ __forceinline__ uint32_t fmix32(uint32_t h) {
     h ^= h >> 16; h *= 0x85ebca6bu; h ^= h >> 13; h *= 0xc2b2ae35u; h ^= h >> 16;
     return h;
 }
-__device__ inline uint32_t term(uint32_t word, uint32_t index) { return fmix32(word ^ (index * 0x9E3779B9u)); }
-__device__ inline uint64_t mix64(uint64_t x) {   // gpu-d1/src/sim.h:15-20
+__device__ __forceinline__ uint32_t term(uint32_t word, uint32_t index) { return fmix32(word ^ (index * 0x9E3779B9u)); }
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {   // gpu-d1/src/sim.h:15-20
     x += 0x9e3779b97f4a7c15ULL;
     x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ULL;
     x = (x ^ (x >> 27)) * 0x94d049bb133111ebULL;
@@ -163,10 +162,11 @@ __device__ inline uint64_t mix64(uint64_t x) {   // gpu-d1/src/sim.h:15-20
 struct Rng {
     uint64_t st, inc;
     uint32_t key0, key1, t, env, dom, k;
-    uint32_t blk, w0, w1, w2, w3;
+    uint32_t blk;
+    unsigned __int128 buf;   // the current Philox block, word j at bits 32j (no indexed fields)
     int mode;
 
-    __device__ void philox_block(uint32_t b) {
+    __device__ __forceinline__ void philox_block(uint32_t b) {
         uint32_t c0 = b, c1 = t, c2 = env, c3 = dom, k0 = key0, k1 = key1;
 #pragma unroll
         for (int r = 0; r < 10; r++) {
@@ -176,10 +176,11 @@ struct Rng {
             c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
             k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
         }
-        w0 = c0; w1 = c1; w2 = c2; w3 = c3;
+        buf = (unsigned __int128)c0 | ((unsigned __int128)c1 << 32) | ((unsigned __int128)c2 << 64) |
+              ((unsigned __int128)c3 << 96);
         blk = b;
     }
-    __device__ uint32_t next() {
+    __device__ __forceinline__ uint32_t next() {
         if (mode == 0) {
             uint64_t old = st;
             st = old * 6364136223846793005ULL + (inc | 1);
@@ -190,9 +191,9 @@ struct Rng {
         if (b != blk) philox_block(b);
         uint32_t j = k & 3u;
         k++;
-        return j == 0 ? w0 : j == 1 ? w1 : j == 2 ? w2 : w3;
+        return (uint32_t)(buf >> (32 * j));
     }
-    __device__ int r(int bound) {   // gpu-d1/src/sim.h:36-51
+    __device__ __forceinline__ int r(int bound) {   // gpu-d1/src/sim.h:36-51
         if (bound <= 1) return 0;
         uint32_t x = next();
         uint64_t m = (uint64_t)x * (uint32_t)bound;
@@ -207,15 +208,15 @@ struct Rng {
         }
         return (int)(m >> 32);
     }
-    __device__ int avg(int n) { int a = r(n); return (a + r(n + 1)) / 2; }             // sim.h:52-55
-    __device__ int round(int n, int d) { int rem = n % d; return n / d + (rem && r(d) < rem); }  // sim.h:56-59
-    __device__ void pcg_seed(uint64_t s, uint64_t seq) {   // sim.h:29-35
+    __device__ __forceinline__ int avg(int n) { int a = r(n); return (a + r(n + 1)) / 2; }             // sim.h:52-55
+    __device__ __forceinline__ int round(int n, int d) { int rem = n % d; return n / d + (rem && r(d) < rem); }  // sim.h:56-59
+    __device__ __forceinline__ void pcg_seed(uint64_t s, uint64_t seq) {   // sim.h:29-35
         mode = 0; st = 0; inc = (seq << 1) | 1;
         next();
         st += s;
         next();
     }
-    __device__ void counter(uint64_t key, uint32_t e, uint32_t tt, uint32_t d) {
+    __device__ __forceinline__ void counter(uint64_t key, uint32_t e, uint32_t tt, uint32_t d) {
         mode = 1; key0 = (uint32_t)key; key1 = (uint32_t)(key >> 32); env = e; t = tt; dom = d; k = 0; blk = 0xFFFFFFFFu;
         st = 0; inc = 0;
     }
@@ -229,7 +230,7 @@ struct Ctx {
     int nslots;
     Rng g;
     int player, hp, regen, blocks, ticks, killed, decisions, floor_seen, episode, first_stair_tick, ncells;
-    int stairs0, stairs1, stairs2;
+    uint64_t stairs;   // three int16 cells at bits 0, 16, 32 (-1 = none)
     uint32_t t, env_id;
     uint64_t vis0, vis1, vis2, vis3;   // player view, quadrants (+,+) (-,+) (-,-) (+,-)
     // this lane's monster (lane < count)
@@ -237,11 +238,14 @@ struct Ctx {
     int lane;
 };
 
-__device__ inline int stair_at(const Ctx &x, int k) { return k == 0 ? x.stairs0 : k == 1 ? x.stairs1 : x.stairs2; }
-__device__ inline bool seen_at(const Ctx &x, int p) { return bit(x.sm->viewed, p) && bit(x.sm->floor, p); }
+__device__ __forceinline__ int stair_at(const Ctx &x, int k) { return (int16_t)(uint16_t)(x.stairs >> (16 * k)); }
+__device__ __forceinline__ uint64_t pack_stairs(int a, int b, int c) {
+    return (uint64_t)(uint16_t)a | (uint64_t)(uint16_t)b << 16 | (uint64_t)(uint16_t)c << 32;
+}
+__device__ __forceinline__ bool seen_at(const Ctx &x, int p) { return bit(x.sm->viewed, p) && bit(x.sm->floor, p); }
 
 // 15x15 view lookup of the cell (dx, dy) from the player
-__device__ inline bool vis_rel(const Ctx &x, int dx, int dy) {
+__device__ __forceinline__ bool vis_rel(const Ctx &x, int dx, int dy) {
     if (iabs(dx) > 7 || iabs(dy) > 7) return false;
     int b = iabs(dy) * 8 + iabs(dx);
     uint64_t v = 0;
@@ -252,23 +256,23 @@ __device__ inline bool vis_rel(const Ctx &x, int dx, int dy) {
     return (v >> b) & 1;
 }
 // in_view, gpu-d1/branches/d1-stairs-v2/src/learn.cu:192-198 (terrain LOS, radius 7)
-__device__ inline bool in_view(const Ctx &x, int p) {
+__device__ __forceinline__ bool in_view(const Ctx &x, int p) {
     if (p < 0) return false;
     return vis_rel(x, p % W - x.player % W, p / W - x.player / W);
 }
-__device__ inline bool q_sx(int q) { return q == 0 || q == 3; }   // +x quadrants
-__device__ inline bool q_sy(int q) { return q < 2; }              // +y quadrants
+__device__ __forceinline__ bool q_sx(int q) { return q == 0 || q == 3; }   // +x quadrants
+__device__ __forceinline__ bool q_sy(int q) { return q < 2; }              // +y quadrants
 
 // Opaque inside-blocker set of quadrant q around (ox, oy): lane j tests blocker
 // (j%8, j/8) (gpu-d1/scripts/compile_fixture.py:35-39; out-of-bounds cells are clear).
-__device__ inline uint64_t opaque_set(const Ctx &x, int ox, int oy, int q) {
+__device__ __forceinline__ uint64_t opaque_set(const Ctx &x, int ox, int oy, int q) {
     int cx = ox + (q_sx(q) ? 1 : -1) * (x.lane & 7), cy = oy + (q_sy(q) ? 1 : -1) * (x.lane >> 3);
     bool op = inb(cx, cy) && !bit_at(x.sm->floor, cx, cy);
     return ballot(op);
 }
 // Player field of view: vis_q bit j set when target (j%8, j/8) of quadrant q is in
 // bounds and one of its rays misses every opaque blocker.
-__device__ void compute_view(Ctx &x) {
+__device__ __forceinline__ void compute_view(Ctx &x) {
     int px = x.player % W, py = x.player / W;
     uint64_t o0 = opaque_set(x, px, py, 0), o1 = opaque_set(x, px, py, 1);
     uint64_t o2 = opaque_set(x, px, py, 2), o3 = opaque_set(x, px, py, 3);
@@ -285,7 +289,7 @@ __device__ void compute_view(Ctx &x) {
 }
 // LOS from a monster to the player within Chebyshev 6 (monster_detects_player,
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:199-207).
-__device__ bool detects(Ctx &x, int origin) {
+__device__ __forceinline__ bool detects(Ctx &x, int origin) {
     int ox = origin % W, oy = origin / W, dx = x.player % W - ox, dy = x.player / W - oy;
     if (iabs(dx) > 6 || iabs(dy) > 6) return false;
     if (!x.c->wake_los) return true;
@@ -303,7 +307,7 @@ __device__ bool detects(Ctx &x, int origin) {
 
 // Reveal, gpu-d1/branches/d1-stairs-v2/src/learn.cu:298-333: viewed |= view; returns
 // the number of floor cells seen for the first time (seen == viewed floor).
-__device__ int reveal(Ctx &x) {
+__device__ __forceinline__ int reveal(Ctx &x) {
     compute_view(x);
     int px = x.player % W, py = x.player / W;
     int fresh = 0;
@@ -329,20 +333,20 @@ __device__ int reveal(Ctx &x) {
     return total;
 }
 
-__device__ inline int stair_index(const Ctx &x) {
+__device__ __forceinline__ int stair_index(const Ctx &x) {
     for (int k = 0; k < 3; k++) if (stair_at(x, k) >= 0 && x.player == stair_at(x, k)) return k + 1;
     return 0;
 }
-__device__ inline int known_stairs(const Ctx &x) {
+__device__ __forceinline__ int known_stairs(const Ctx &x) {
     int n = 0;
     for (int k = 0; k < 3; k++) n += stair_at(x, k) >= 0 && seen_at(x, stair_at(x, k));
     return n;
 }
-__device__ inline bool visible_awake(const Ctx &x) {
+__device__ __forceinline__ bool visible_awake(const Ctx &x) {
     bool me = x.lane < x.c->count && x.mhp > 0 && x.mawake && in_view(x, x.mpos);
     return ballot(me) != 0;
 }
-__device__ inline void occ_set(Ctx &x, int p, bool on) {
+__device__ __forceinline__ void occ_set(Ctx &x, int p, bool on) {
     if (x.lane == 0) {
         uint32_t *w = &x.sm->occ[(p / W) * RW + ((p % W) >> 5)];
         uint32_t b = 1u << ((p % W) & 31);
@@ -353,7 +357,7 @@ __device__ inline void occ_set(Ctx &x, int p, bool on) {
 
 // ---------------------------------------------------------------- cell selection
 // Row prefix counts of a bitmap (rows in `bm`), stored inclusive in sm->rowpre.
-__device__ int row_prefix(Ctx &x, const uint32_t *bm) {
+__device__ __forceinline__ int row_prefix(Ctx &x, const uint32_t *bm) {
     int y0 = x.lane, y1 = x.lane + 64;
     int c0 = row_popc(row_ld(bm, y0));
     int c1 = y1 < H ? row_popc(row_ld(bm, y1)) : 0;
@@ -369,7 +373,7 @@ __device__ int row_prefix(Ctx &x, const uint32_t *bm) {
     return x.sm->rowpre[H - 1];
 }
 // The k-th set cell (row-major) of bitmap `bm`, given its rowpre.
-__device__ int select_cell(Ctx &x, const uint32_t *bm, int k) {
+__device__ __forceinline__ int select_cell(Ctx &x, const uint32_t *bm, int k) {
     int lo = 0, hi = H - 1;   // first row with rowpre > k
     while (lo < hi) { int mid = (lo + hi) >> 1; if (x.sm->rowpre[mid] > k) hi = mid; else lo = mid + 1; }
     int before = lo ? x.sm->rowpre[lo - 1] : 0;
@@ -381,7 +385,7 @@ __device__ int select_cell(Ctx &x, const uint32_t *bm, int k) {
 // rejection with the v1 HP table gpu-d1/src/learn.cu:305-314, then three stairs by
 // reservoir choice from a copy of the RNG, then the initial reveal without reward).
 // roster_mode 1 and awake_pct draw after the energy draw.
-__device__ void reset(Ctx &x, const uint32_t *cells_g) {
+__device__ __forceinline__ void reset(Ctx &x, const uint32_t *cells_g) {
     Smem *sm = x.sm;
     const D1Config *c = x.c;
     for (int w = x.lane; w < ROWS_WORDS; w += 64) { sm->occ[w] = 0; sm->front[w] = cells_g[w]; sm->viewed[w] = 0; }
@@ -415,7 +419,7 @@ __device__ void reset(Ctx &x, const uint32_t *cells_g) {
     // Stairs: a copy of the RNG, reservoir over eligible cells in cell order.
     Rng s = x.g;
     x.first_stair_tick = -1;
-    x.stairs0 = x.stairs1 = x.stairs2 = -1;
+    x.stairs = pack_stairs(-1, -1, -1);
     int px = x.player % W, py = x.player / W;
     for (int k = 0; k < 3; k++) {
         if (k >= c->stairs) break;
@@ -435,14 +439,14 @@ __device__ void reset(Ctx &x, const uint32_t *cells_g) {
         for (int cnt = 1; cnt <= total; cnt++)
             if (s.r(cnt) == 0) chosen = cnt - 1;
         int sel = chosen >= 0 ? select_cell(x, sm->reach, chosen) : -1;
-        if (k == 0) x.stairs0 = sel; else if (k == 1) x.stairs1 = sel; else x.stairs2 = sel;
+        x.stairs = (x.stairs & ~(0xFFFFULL << (16 * k))) | (uint64_t)(uint16_t)sel << (16 * k);
         __syncthreads();
     }
     reveal(x);
 }
 
 // ---------------------------------------------------------------- monsters
-__device__ inline int kind_speed(const D1Config *c, int k) {
+__device__ __forceinline__ int kind_speed(const D1Config *c, int k) {
     int s = c->kinds[0].speed;
     s = k == 1 ? c->kinds[1].speed : s;
     s = k == 2 ? c->kinds[2].speed : s;
@@ -452,7 +456,7 @@ __device__ inline int kind_speed(const D1Config *c, int k) {
     return s;
 }
 // gpu-d1/src/sim.h:130-163 (kind = the acting monster's kind)
-__device__ void attack(Ctx &x, int kind) {
+__device__ __forceinline__ void attack(Ctx &x, int kind) {
     const D1Config *c = x.c;
     const D1Kind &k = c->kinds[kind];
     Rng &r = x.g;
@@ -477,16 +481,16 @@ __device__ void attack(Ctx &x, int kind) {
     x.hp -= damage;
 }
 // distance of q relative to p (both via the BFS field); BIG when q was not reached
-__device__ inline int rel_dist(const Ctx &x, int q, int p) {
+__device__ __forceinline__ int rel_dist(const Ctx &x, int q, int p) {
     if (!bit(x.sm->reach, q)) return BIG;
     return (int)(int8_t)(uint8_t)(x.sm->dist[q] - x.sm->dist[p]);
 }
-__device__ inline bool walkable(const Ctx &x, int q) {
+__device__ __forceinline__ bool walkable(const Ctx &x, int q) {
     return q >= 0 && bit(x.sm->floor, q) && q != x.player && !bit(x.sm->occ, q);
 }
 // gpu-d1/src/sim.h:207-253: greedy descent with rotated order and 1/ties
 // replacement, then a bounded 24-node BFS detour when stuck.
-__device__ int choose_move(Ctx &x, int p) {
+__device__ __forceinline__ int choose_move(Ctx &x, int p) {
     int rotation = x.g.r(4);
     int z = x.lane & 7;
     int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
@@ -524,10 +528,33 @@ __device__ int choose_move(Ctx &x, int p) {
     }
     return -1;
 }
+// One BFS layer for row y: dilate the frontier rows y-1..y+1 by one cell, keep floor
+// cells not reached yet.
+__device__ __forceinline__ Row bfs_expand(const Smem *sm, int y) {
+    Row v = row_ld(sm->front, y);
+    if (y > 0) v = row_or(v, row_ld(sm->front, y - 1));
+    if (y < H - 1) v = row_or(v, row_ld(sm->front, y + 1));
+    v = row_or(v, row_or(row_shl1(v), row_shr1(v)));
+    return row_andn(row_and(v, row_ld(sm->floor, y)), row_ld(sm->reach, y));
+}
+__device__ __forceinline__ void scatter_layer(Smem *sm, int base, uint32_t b, int layer) {
+    while (b) {
+        int xx = __ffs(b) - 1;
+        b &= b - 1;
+        sm->dist[base + xx] = (uint8_t)layer;
+    }
+}
+__device__ __forceinline__ void bfs_commit(Smem *sm, int y, Row nw, int layer) {
+    row_st(sm->front, y, nw);
+    row_st(sm->reach, y, row_or(row_ld(sm->reach, y), nw));
+    scatter_layer(sm, y * W, nw.a, layer);
+    scatter_layer(sm, y * W + 32, nw.b, layer);
+    scatter_layer(sm, y * W + 64, nw.c, layer);
+}
 // Bit-parallel BFS over floor from the player (the all-pairs row of
 // gpu-d1/scripts/learn_env.py:31-39), stopped `margin` layers after every mover is
 // reached. dist holds the layer mod 256; comparisons are relative (|delta| <= 25).
-__device__ void bfs(Ctx &x, uint64_t movers, int margin) {
+__device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
     Smem *sm = x.sm;
     for (int w = x.lane; w < ROWS_WORDS; w += 64) { sm->reach[w] = 0; sm->front[w] = 0; }
     __syncthreads();
@@ -539,40 +566,14 @@ __device__ void bfs(Ctx &x, uint64_t movers, int margin) {
     }
     __syncthreads();
     int stop = 1 << 30;
+    const int y0 = x.lane, y1 = x.lane + 64;
     for (int layer = 1; layer < N; layer++) {
-        Row nw[2];
-        for (int s = 0; s < 2; s++) {
-            int y = x.lane + 64 * s;
-            nw[s] = Row{0, 0, 0};
-            if (y < H) {
-                Row v = row_ld(sm->front, y);
-                if (y > 0) v = row_or(v, row_ld(sm->front, y - 1));
-                if (y < H - 1) v = row_or(v, row_ld(sm->front, y + 1));
-                v = row_or(v, row_or(row_shl1(v), row_shr1(v)));
-                nw[s] = row_andn(row_and(v, row_ld(sm->floor, y)), row_ld(sm->reach, y));
-            }
-        }
+        Row n0 = bfs_expand(sm, y0), n1 = y1 < H ? bfs_expand(sm, y1) : Row{0, 0, 0};
         __syncthreads();
-        bool any = false;
-        for (int s = 0; s < 2; s++) {
-            int y = x.lane + 64 * s;
-            if (y < H) {
-                row_st(sm->front, y, nw[s]);
-                row_st(sm->reach, y, row_or(row_ld(sm->reach, y), nw[s]));
-                uint32_t ws[3] = {nw[s].a, nw[s].b, nw[s].c};
-                for (int k = 0; k < 3; k++) {
-                    uint32_t b = ws[k];
-                    while (b) {
-                        int xx = 32 * k + __ffs(b) - 1;
-                        b &= b - 1;
-                        sm->dist[y * W + xx] = (uint8_t)layer;
-                    }
-                }
-                any |= row_any(nw[s]);
-            }
-        }
+        bfs_commit(sm, y0, n0, layer);
+        if (y1 < H) bfs_commit(sm, y1, n1, layer);
         __syncthreads();
-        if (!ballot(any)) break;
+        if (!ballot(row_any(n0) || row_any(n1))) break;
         if (stop == (1 << 30)) {
             bool missing = ((movers >> x.lane) & 1) && !bit(sm->reach, x.mpos);
             if (!ballot(missing)) stop = layer + margin;
@@ -581,7 +582,7 @@ __device__ void bfs(Ctx &x, uint64_t movers, int margin) {
     }
 }
 // gpu-d1/src/sim.h:254-269
-__device__ void act(Ctx &x, int id) {
+__device__ __forceinline__ void act(Ctx &x, int id) {
     if (x.lane == id) x.menergy -= 10;
     int p = lane_val(x.mpos, id);
     if (cheb(p, x.player) == 1) { attack(x, lane_val(x.mkind, id)); return; }
@@ -597,7 +598,7 @@ __device__ void act(Ctx &x, int id) {
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:684-827 with the v1 kill-all clear
 // (gpu-d1/src/learn.cu:549) as a switch. d: 0-7 move/bump, 8 wait, 18 descend.
 // Returns done; out8 = reward, done, clear, killed, hp, ticks, death, timeout.
-__device__ bool primitive(Ctx &x, int d, float *out8, bool &saw, const uint32_t *cells_g) {
+__device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw, const uint32_t *cells_g) {
     const D1Config *c = x.c;
     Smem *sm = x.sm;
     int milli = c->step_milli;
@@ -667,7 +668,7 @@ __device__ bool primitive(Ctx &x, int d, float *out8, bool &saw, const uint32_t 
 }
 
 // Joint action, gpu-d1/branches/d1-stairs-v2/src/learn.cu:852-875.
-__device__ void transition(Ctx &x, int action, float *out, const uint32_t *cells_g) {
+__device__ __forceinline__ void transition(Ctx &x, int action, float *out, const uint32_t *cells_g) {
     const D1Config *c = x.c;
     int decisions = x.decisions + 1;
     bool invalid = false;
@@ -699,7 +700,7 @@ __device__ void transition(Ctx &x, int action, float *out, const uint32_t *cells
 // 6 remembered stair, 7 frontier anchor (seen floor with an in-bounds unviewed
 // neighbour; the FRONTIER_RING_MEMORY_WALLS rule of
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:269-280).
-__device__ void write_obs(Ctx &x, uint8_t *o) {
+__device__ __forceinline__ void write_obs(Ctx &x, uint8_t *o) {
     Smem *sm = x.sm;
     int px = x.player % W, py = x.player / W;
     // frontier rows of the window into sm->front
@@ -723,11 +724,11 @@ __device__ void write_obs(Ctx &x, uint8_t *o) {
             sm->win[(dy + 7) * 15 + dx + 7] = (uint32_t)(x.mkind + 1) | ((uint32_t)imin(x.mhp, 255) << 8);
     }
     __syncthreads();
-    if (x.lane < 3) {
-        int sp = x.lane == 0 ? x.stairs0 : x.lane == 1 ? x.stairs1 : x.stairs2;
-        if (sp >= 0) {
+    for (int k = 0; k < 3; k++) {
+        int sp = stair_at(x, k);
+        if (x.lane == 0 && sp >= 0) {
             int dx = sp % W - px, dy = sp / W - py;
-            if (iabs(dx) <= 7 && iabs(dy) <= 7) atomicOr(&sm->win[(dy + 7) * 15 + dx + 7], 1u << 16);
+            if (iabs(dx) <= 7 && iabs(dy) <= 7) sm->win[(dy + 7) * 15 + dx + 7] |= 1u << 16;
         }
     }
     __syncthreads();
@@ -750,29 +751,15 @@ __device__ void write_obs(Ctx &x, uint8_t *o) {
 }
 // Sum over canonical words of fmix32(word ^ index*0x9E3779B9) (index map in
 // include/d1hip.h's companion spec: scalars 0-14, monsters 100+2i, viewed 1000+3y+j).
-__device__ uint32_t state_hash(Ctx &x) {
-    uint32_t h = 0;
-    if (x.lane < 15) {
-        uint32_t w;
-        switch (x.lane) {
-        case 0: w = (uint32_t)x.player; break;
-        case 1: w = (uint32_t)x.hp; break;
-        case 2: w = (uint32_t)x.regen; break;
-        case 3: w = (uint32_t)x.ticks; break;
-        case 4: w = (uint32_t)x.killed; break;
-        case 5: w = (uint32_t)x.decisions; break;
-        case 6: w = (uint32_t)x.floor_seen; break;
-        case 7: w = (uint32_t)x.episode; break;
-        case 8: w = x.g.mode == 0 ? (uint32_t)x.g.st : 0u; break;
-        case 9: w = x.g.mode == 0 ? (uint32_t)(x.g.st >> 32) : 0u; break;
-        case 10: w = x.t; break;
-        case 11: w = (uint32_t)x.stairs0; break;
-        case 12: w = (uint32_t)x.stairs1; break;
-        case 13: w = (uint32_t)x.stairs2; break;
-        default: w = (uint32_t)x.first_stair_tick; break;
-        }
-        h += term(w, (uint32_t)x.lane);
-    }
+__device__ __forceinline__ uint32_t state_hash(Ctx &x) {
+    // scalar words are hashed in uniform code and added once (lane 0)
+    uint32_t scal = term((uint32_t)x.player, 0) + term((uint32_t)x.hp, 1) + term((uint32_t)x.regen, 2) +
+                    term((uint32_t)x.ticks, 3) + term((uint32_t)x.killed, 4) + term((uint32_t)x.decisions, 5) +
+                    term((uint32_t)x.floor_seen, 6) + term((uint32_t)x.episode, 7) +
+                    term(x.g.mode == 0 ? (uint32_t)x.g.st : 0u, 8) + term(x.g.mode == 0 ? (uint32_t)(x.g.st >> 32) : 0u, 9) +
+                    term(x.t, 10) + term((uint32_t)stair_at(x, 0), 11) + term((uint32_t)stair_at(x, 1), 12) +
+                    term((uint32_t)stair_at(x, 2), 13) + term((uint32_t)x.first_stair_tick, 14);
+    uint32_t h = x.lane == 0 ? scal : 0u;
     if (x.lane < x.c->count) {
         h += term((uint16_t)x.mpos | (uint32_t)(uint16_t)x.mhp << 16, 100 + 2 * x.lane);
         h += term((uint16_t)x.menergy | (uint32_t)x.mawake << 16 | (uint32_t)x.mkind << 24, 101 + 2 * x.lane);
@@ -783,12 +770,12 @@ __device__ uint32_t state_hash(Ctx &x) {
 }
 
 // ---------------------------------------------------------------- load / store
-__device__ void load_world(Ctx &x, const uint8_t *row, int max_m) {
+__device__ __forceinline__ void load_world(Ctx &x, const uint8_t *row, int max_m) {
     Hdr h = *(const Hdr *)row;
     x.player = h.player; x.hp = h.hp; x.regen = h.regen; x.ncells = h.ncells;
     x.ticks = h.ticks; x.killed = h.killed; x.decisions = h.decisions; x.floor_seen = h.floor_seen;
     x.episode = h.episode; x.first_stair_tick = h.first_stair_tick;
-    x.stairs0 = h.stairs[0]; x.stairs1 = h.stairs[1]; x.stairs2 = h.stairs[2];
+    x.stairs = pack_stairs(h.stairs[0], h.stairs[1], h.stairs[2]);
     x.blocks = h.blocks; x.t = h.t; x.env_id = h.env_id;
     if (x.c->rng_mode == 0) { x.g.mode = 0; x.g.st = h.rng_state; x.g.inc = h.rng_inc; }
     else x.g.counter(h.rng_state, h.env_id, h.t, 0);
@@ -803,7 +790,7 @@ __device__ void load_world(Ctx &x, const uint8_t *row, int max_m) {
         atomicOr(&x.sm->occ[(x.mpos / W) * RW + ((x.mpos % W) >> 5)], 1u << ((x.mpos % W) & 31));
     __syncthreads();
 }
-__device__ void store_world(Ctx &x, uint8_t *row, int max_m) {
+__device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
     if (x.lane == 0) {
         Hdr h;
         h.rng_state = x.g.mode == 0 ? x.g.st : ((uint64_t)x.g.key1 << 32 | x.g.key0);
@@ -811,7 +798,7 @@ __device__ void store_world(Ctx &x, uint8_t *row, int max_m) {
         h.env_id = x.env_id; h.t = x.t; h.episode = x.episode;
         h.player = (int16_t)x.player; h.hp = (int16_t)x.hp; h.regen = (int16_t)x.regen; h.ncells = (int16_t)x.ncells;
         h.ticks = x.ticks; h.killed = x.killed; h.decisions = x.decisions; h.floor_seen = x.floor_seen;
-        h.stairs[0] = (int16_t)x.stairs0; h.stairs[1] = (int16_t)x.stairs1; h.stairs[2] = (int16_t)x.stairs2;
+        h.stairs[0] = (int16_t)stair_at(x, 0); h.stairs[1] = (int16_t)stair_at(x, 1); h.stairs[2] = (int16_t)stair_at(x, 2);
         h.blocks = (int16_t)x.blocks; h.first_stair_tick = x.first_stair_tick;
         *(Hdr *)row = h;
     }
@@ -828,7 +815,7 @@ __device__ void store_world(Ctx &x, uint8_t *row, int max_m) {
 // ---------------------------------------------------------------- level generator
 // Build-owned spec (see oracle/d1_oracle.c o_level_generate): 3x3 sectors, 6-9
 // rooms by partial Fisher-Yates, L corridors between consecutive centres.
-__device__ void generate_level(Ctx &x, uint64_t seed, uint32_t env, uint32_t *floor_rows) {
+__device__ __forceinline__ void generate_level(Ctx &x, uint64_t seed, uint32_t env, uint32_t *floor_rows) {
     Rng g;
     g.counter(seed, env, 0, 1);
     int n = 6 + g.r(4);
@@ -889,12 +876,14 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
         for (int s = 0; s < 2; s++) {
             int y = x.lane + 64 * s;
             if (y >= H) break;
-            uint32_t f[3] = {0, 0, 0}, cc[3] = {0, 0, 0};
-            for (int xx = 0; xx < W; xx++) {
-                f[xx >> 5] |= (uint32_t)(tab.floor[y * W + xx] != 0) << (xx & 31);
-                cc[xx >> 5] |= (uint32_t)(tab.cells[y * W + xx] != 0) << (xx & 31);
+            for (int j = 0; j < 3; j++) {
+                uint32_t f = 0, cc = 0;
+                for (int b = 0; b < 32 && 32 * j + b < W; b++) {
+                    f |= (uint32_t)(tab.floor[y * W + 32 * j + b] != 0) << b;
+                    cc |= (uint32_t)(tab.cells[y * W + 32 * j + b] != 0) << b;
+                }
+                sm.floor[y * RW + j] = f; fg[y * RW + j] = f; cg[y * RW + j] = cc;
             }
-            for (int j = 0; j < 3; j++) { sm.floor[y * RW + j] = f[j]; fg[y * RW + j] = f[j]; cg[y * RW + j] = cc[j]; }
         }
     }
     __syncthreads();
