@@ -58,9 +58,13 @@ struct Smem {
     uint32_t occ[ROWS_WORDS];
     uint32_t reach[ROWS_WORDS];
     uint32_t front[ROWS_WORDS];
-    uint32_t win[225];          // observation window: kind+1 | hp<<8 | stair<<16
-    int32_t rowpre[72];         // inclusive per-row prefix counts for cell selection
-    uint8_t dist[N];            // BFS layer mod 256, valid where `reach` is set
+    union {
+        uint8_t dist[N];        // BFS layer mod 256, valid where `reach` is set (monster phase)
+        struct {
+            uint32_t win[225];  // observation window: kind+1 | hp<<8 | stair<<16 (observation)
+            int32_t rowpre[72]; // inclusive per-row prefix counts (episode reset)
+        };
+    };
 };
 
 // ---------------------------------------------------------------- small helpers
@@ -222,6 +226,57 @@ struct Rng {
     }
 };
 
+// PCG jump-ahead: state after j steps = A[j]*s + C[j]*inc (A[j] = a^j, C[j] = sum_{i<j} a^i).
+struct PcgJump {
+    uint64_t a[65], c[65];
+    constexpr PcgJump() : a(), c() {
+        a[0] = 1; c[0] = 0;
+        for (int j = 1; j <= 64; j++) { a[j] = a[j - 1] * 6364136223846793005ULL; c[j] = c[j - 1] * 6364136223846793005ULL + 1; }
+    }
+};
+__constant__ constexpr PcgJump kJump{};
+
+__device__ __forceinline__ uint32_t pcg_out(uint64_t old) {
+    uint32_t x = (uint32_t)(((old >> 18) ^ old) >> 27), r = (uint32_t)(old >> 59);
+    return (x >> r) | (x << ((0u - r) & 31u));
+}
+// Reservoir choice over `total` eligible cells: the 1-based count c is kept when
+// r(c) == 0, the last kept count wins (gpu-d1/branches/d1-stairs-v2/src/learn.cu:432-441).
+// 64 counts per pass: lane l evaluates count c0+l from the draw it would get if no
+// earlier draw in the pass were rejected; a pass in which any Lemire rejection is
+// possible (low < bound) is replayed serially, so the draw sequence is the serial one.
+__device__ __forceinline__ int reservoir(Rng &s, int total, int lane) {
+    int chosen = total >= 1 ? 0 : -1;
+    int c0 = 2;
+    while (c0 <= total) {
+        int cnt = imin(64, total - c0 + 1);
+        int c = c0 + lane;
+        uint32_t xw;
+        if (s.mode == 0) {
+            uint64_t old = kJump.a[lane] * s.st + kJump.c[lane] * s.inc;
+            xw = pcg_out(old);
+        } else {
+            uint32_t kk = s.k + (uint32_t)lane;
+            Rng tmp = s;
+            tmp.philox_block(kk >> 2);
+            xw = (uint32_t)(tmp.buf >> (32 * (kk & 3u)));
+        }
+        uint64_t m = (uint64_t)xw * (uint32_t)c;
+        bool act = lane < cnt;
+        bool risky = act && (uint32_t)m < (uint32_t)c;
+        if (ballot(risky)) {
+            for (int cc = c0; cc < c0 + cnt; cc++) if (s.r(cc) == 0) chosen = cc - 1;
+        } else {
+            uint64_t keep = ballot(act && (m >> 32) == 0);
+            if (keep) chosen = c0 + 63 - __clzll((long long)keep) - 1;
+            if (s.mode == 0) s.st = kJump.a[cnt] * s.st + kJump.c[cnt] * s.inc;
+            else s.k += (uint32_t)cnt;
+        }
+        c0 += cnt;
+    }
+    return chosen;
+}
+
 // ---------------------------------------------------------------- world context
 struct Ctx {
     Smem *sm;
@@ -233,6 +288,7 @@ struct Ctx {
     uint64_t stairs;   // three int16 cells at bits 0, 16, 32 (-1 = none)
     uint32_t t, env_id;
     uint64_t vis0, vis1, vis2, vis3;   // player view, quadrants (+,+) (-,+) (-,-) (+,-)
+    bool adj_clear;                     // the 8 neighbours of any cell are always in view
     // this lane's monster (lane < count)
     int mpos, mhp, menergy, mawake, mkind;
     int lane;
@@ -435,9 +491,7 @@ __device__ __forceinline__ void reset(Ctx &x, const uint32_t *cells_g) {
         }
         __syncthreads();
         int total = row_prefix(x, sm->reach);
-        int chosen = -1;
-        for (int cnt = 1; cnt <= total; cnt++)
-            if (s.r(cnt) == 0) chosen = cnt - 1;
+        int chosen = reservoir(s, total, x.lane);
         int sel = chosen >= 0 ? select_cell(x, sm->reach, chosen) : -1;
         x.stairs = (x.stairs & ~(0xFFFFULL << (16 * k))) | (uint64_t)(uint16_t)sel << (16 * k);
         __syncthreads();
@@ -677,7 +731,7 @@ __device__ __forceinline__ void transition(Ctx &x, int action, float *out, const
         int d = 8;
         if (action >= 0 && action < 16) {
             int dir = action % 8, p = nbr(x.player, dir);
-            bool enemy = p >= 0 && in_view(x, p) && bit(x.sm->occ, p);
+            bool enemy = p >= 0 && (x.adj_clear || in_view(x, p)) && bit(x.sm->occ, p);
             bool valid = action < 8 ? p >= 0 && (!bit(x.sm->viewed, p) || bit(x.sm->floor, p)) && !enemy : enemy;
             if (valid) d = dir; else invalid = true;
         } else if (action == 17) invalid = x.hp >= c->hp || visible_awake(x) || c->regen <= 0;
@@ -866,6 +920,7 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
     uint8_t *row = state + (size_t)env * row_bytes;
     Ctx x;
     x.sm = &sm; x.c = &cfg; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
+    x.adj_clear = false;
     uint32_t *fg = (uint32_t *)(row + off_floor(max_m));
     uint32_t *cg = (uint32_t *)(row + off_cells(max_m));
     if (cfg.level_mode == 1) {
@@ -911,9 +966,12 @@ __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, s
     x.sm = &sm; x.c = &cfg; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
     load_world(x, row, max_m);
     const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
-    compute_view(x);
     int64_t a = actions[env];
     int action = a < 0 || a > 1000 ? -1 : (int)a;
+    // Adjacent cells are visible whenever their first ray has no blocker (true of the
+    // native table); then only REST needs the full view before the player acts.
+    x.adj_clear = tab.ray_slots[1] == 0 && tab.ray_slots[8] == 0 && tab.ray_slots[9] == 0;
+    if (!x.adj_clear || action == 17) compute_view(x);
     float o8[8];
     transition(x, action, o8, cg);
     x.t++;
