@@ -69,6 +69,26 @@ __global__ __launch_bounds__(256) void k_gae(const float *__restrict__ reward, c
     }
 }
 
+// uint8 -> bf16 widening of the observation batch (exact: every byte value has at most
+// 8 significant bits). 16 bytes in, 32 bytes out per lane.
+__global__ __launch_bounds__(256) void k_u8_bf16(const uint4 *__restrict__ in, uint4 *__restrict__ out, size_t n16) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n16) return;
+    uint4 v = in[i];
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t b0 = (w[j] >> (16 * h)) & 0xFFu, b1 = (w[j] >> (16 * h + 8)) & 0xFFu;
+            o[2 * j + h] = (__float_as_uint((float)b0) >> 16) | (__float_as_uint((float)b1) & 0xFFFF0000u);
+        }
+    }
+    out[2 * i] = make_uint4(o[0], o[1], o[2], o[3]);
+    out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 }  // namespace d1p
 
 extern "C" {
@@ -78,6 +98,15 @@ int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t
     if (n == 0) return 0;
     hipLaunchKernelGGL(d1p::k_sample, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, logits, n, k, ld,
                        (uint32_t)seed, (uint32_t)(seed >> 32), t, actions, logp);
+    return (int)hipGetLastError();
+}
+int d1_obs_to_bf16(const uint8_t *obs, void *out, int64_t count, void *stream) {
+    if (count < 0 || (count % 16) || (count && (!obs || !out))) return D1_E_ARG;
+    if (((uintptr_t)obs & 15) || ((uintptr_t)out & 15)) return D1_E_ARG;
+    if (count == 0) return 0;
+    size_t n16 = (size_t)count / 16;
+    hipLaunchKernelGGL(d1p::k_u8_bf16, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4 *)obs, (uint4 *)out, n16);
     return (int)hipGetLastError();
 }
 int d1_gae(const float *reward, const uint8_t *done, const float *value, const float *bootstrap, int T, int n,

@@ -31,11 +31,30 @@ class Policy(nn.Module):
 
     def forward(self, obs_u8):
         """obs uint8 [B, 15, 15, 8] (or [B, 1800]) -> (fp32 logits [B, A], fp32 value [B])."""
-        x = obs_u8.reshape(obs_u8.shape[0], -1).to(self.l1.weight.dtype)
-        h = torch.relu(self.l1(x))
-        h = torch.relu(self.l2(h))
+        x = widen(obs_u8.reshape(obs_u8.shape[0], -1), self.l1.weight.dtype)
+        if x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_grad_enabled():
+            # bias + ReLU in the hipBLASLt epilogue
+            h = torch._addmm_activation(self.l1.bias, x, self.l1.weight.t())
+            h = torch._addmm_activation(self.l2.bias, h, self.l2.weight.t())
+        else:
+            h = torch.relu(self.l1(x))
+            h = torch.relu(self.l2(h))
         out = self.head(h).float()
         return out[:, :self.n_actions], out[:, self.n_actions]
+
+
+def widen(obs_u8, dtype):
+    """uint8 observations -> `dtype`; the bf16 case runs the HIP widening kernel."""
+    if obs_u8.dtype != torch.uint8:
+        return obs_u8.to(dtype)
+    if dtype == torch.bfloat16 and obs_u8.is_cuda and obs_u8.is_contiguous() and obs_u8.numel() % 16 == 0 \
+            and obs_u8.data_ptr() % 16 == 0:
+        out = torch.empty(obs_u8.shape, dtype=dtype, device=obs_u8.device)
+        L = _lib.load()
+        _lib.check(L.d1_obs_to_bf16(obs_u8.data_ptr(), out.data_ptr(), obs_u8.numel(),
+                                    torch.cuda.current_stream(obs_u8.device).cuda_stream), 'd1_obs_to_bf16')
+        return out
+    return obs_u8.to(dtype)
 
 
 def sample(logits, seed, t, actions=None, logp=None):

@@ -113,6 +113,10 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
 int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t t,
               int64_t *actions, float *logp, void *stream);
 
+/* Widen `count` uint8 observation bytes to bf16 (exact), for the policy trunk.
+ * count must be a multiple of 16 and both pointers 16-byte aligned. */
+int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stream);
+
 /* Reverse-time GAE over a [T, n] rollout (gpu-d1/scripts/run_ring_ablations.py:354-360):
  *   live = 1 - done[t]; delta = reward[t] + (gamma*next)*live - value[t];
  *   gae = delta + (gamma_lambda*live)*gae; adv[t] = gae; next = value[t]

@@ -97,3 +97,26 @@ def test_gae_properties_closed_form():
     d[5] = 1      # a done cuts the bootstrap and the accumulation at t=5
     adv, _ = pol.gae(r.cuda(), d.cuda(), v.cuda(), boot.cuda(), gamma=1.0, lam=1.0)
     assert torch.equal(adv.cpu()[5], r[5] - v[5])
+
+
+def test_widening_is_exact():
+    pol = importlib.import_module('dcss-auto_amd.policy')
+    x = torch.arange(256, dtype=torch.uint8).repeat(4096 * 7 // 256 + 16)[: 4096 * 7].cuda()
+    y = pol.widen(x, torch.bfloat16)
+    assert torch.equal(y.float().cpu(), x.float().cpu())
+
+
+def test_policy_forward_matches_fp32_reference():
+    """bf16 trunk vs an fp32 restatement with the same (bf16-rounded) weights: 2e-2."""
+    pol = importlib.import_module('dcss-auto_amd.policy')
+    model = pol.Policy(seed=3).cuda().to(torch.bfloat16)
+    obs = torch.randint(0, 20, (512, 15, 15, 8), dtype=torch.uint8, device='cuda')
+    with torch.no_grad():
+        logits, value = model(obs)
+        x = obs.reshape(512, -1).float()
+        w = {k: v.float() for k, v in model.state_dict().items()}
+        h = torch.relu(x @ w['l1.weight'].t() + w['l1.bias'])
+        h = torch.relu(h @ w['l2.weight'].t() + w['l2.bias'])
+        out = h @ w['head.weight'].t() + w['head.bias']
+    torch.testing.assert_close(logits, out[:, :16], rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(value, out[:, 16], rtol=2e-2, atol=2e-2)
