@@ -59,6 +59,55 @@ def cpu_baseline(envs=1024, steps=1000, threads=None):
                       f'step+obs+hash, {dt:.2f} s wall'}
 
 
+def ppo_bench(args, env, rollout_model, policy_mod, dev):
+    """C4: a real T x N rollout fills the buffer (obs written in place by the env), then
+    rewards/dones/values are replaced by C4's synthetic draws (r = 0 w.p. 0.97 else
+    U(-1,1), done ~ Bernoulli(0.01), v ~ N(0,1)); the timed region is GAE + advantage
+    normalisation + 4 epochs of 8,192-sample minibatch updates (fwd+bwd+clip+Adam)."""
+    import torch
+    ppo_mod = importlib.import_module('dcss-auto_amd.ppo')
+    T, n = args.horizon, args.envs
+    buf = ppo_mod.RolloutBuffer(T, n, device=dev)
+    actions = torch.zeros(n, dtype=torch.int64, device=dev)
+    with torch.no_grad():
+        obs = env.obs
+        for t in range(T):
+            buf.obs[t].copy_(obs.view(n, -1))
+            logits, value = rollout_model(obs)
+            policy_mod.sample(logits, 7, t, actions, buf.logp[t])
+            buf.actions[t].copy_(actions)
+            obs, _ = env.step(actions)
+    g = torch.Generator(device=dev).manual_seed(4)
+    buf.rewards.copy_(torch.where(torch.rand(T, n, device=dev, generator=g) < 0.97, 0.0,
+                                  torch.rand(T, n, device=dev, generator=g) * 2 - 1))
+    buf.dones.copy_((torch.rand(T, n, device=dev, generator=g) < 0.01).to(torch.uint8))
+    buf.values.copy_(torch.randn(T, n, device=dev, generator=g))
+    buf.bootstrap.copy_(torch.randn(n, device=dev, generator=g))
+    model = policy_mod.Policy(seed=0).to(dev)           # fp32 master weights
+    if args.eager_ppo:
+        trainer = ppo_mod.PPO(model)                     # torch autograd + fused Adam, eager
+        trainer.update(ppo_mod.RolloutBuffer(2, 8192, device=dev))   # warm the eager path
+    else:
+        trainer = ppo_mod.FastPPO(model, graph=True)     # explicit fwd/bwd, HIP-graph minibatch step
+        trainer._capture(buf)                            # capture once per buffer, outside the timing
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    loss = trainer.update(buf, generator=torch.Generator(device=dev).manual_seed(5))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    samples = T * n
+    flops = samples * trainer.epochs * (TRUNK_FLOPS + 2 * (1800 * 256 + 2 * 256 * 256 + 2 * 256 * 17))
+    return {'metric': 'PPO samples/sec (C4: GAE + 4 epochs x 8,192-sample minibatches)', 'value': samples / dt,
+            'unit': 'samples/s', 'sample_epochs_per_s': samples * trainer.epochs / dt, 'update_s': dt,
+            'n_gpus': 1, 'higher_is_better': True, 'dtype': 'bf16 trunk, fp32 master',
+            'loss_terms': [float(v) for v in torch.as_tensor(loss).flatten()[:3]], 'graph': trainer.graph,
+            'path': 'autograd eager' if args.eager_ppo else 'explicit fwd/bwd, HIP graph',
+            'config': {'workload': 'C4', 'T': T, 'envs': n, 'epochs': trainer.epochs, 'minibatch': trainer.minibatch,
+                       'gamma': 0.99, 'lambda': 0.95, 'clip': 0.2, 'vcoef': 0.5, 'ecoef': 0.01},
+            'mfma': {'achieved': flops / dt / 1e12, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': flops / dt / 1e12 / BF16_PEAK_TFLOPS}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -67,8 +116,11 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters'], default='rollout',
-                    help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc')
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo'], default='rollout',
+                    help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
+                         'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer')
+    ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
+    ap.add_argument('--eager-ppo', action='store_true', help='run the PPO update without HIP-graph capture')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
@@ -95,6 +147,10 @@ def main():
             env.step(actions)
         torch.cuda.synchronize()
         print(json.dumps({'mode': 'counters', 'copy_bytes': src.numel() * 4, 'env_steps': args.steps, 'envs': n}))
+        return
+
+    if args.mode == 'ppo':
+        print(json.dumps(ppo_bench(args, env, model, policy_mod, dev)), flush=True)
         return
 
     def one_step(t, ev=None):

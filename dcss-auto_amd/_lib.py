@@ -9,7 +9,8 @@ LIB_PATH = HERE / 'libd1hip.so'
 _LIB = None
 
 SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
-           'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16')
+           'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16',
+           'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd', 'd1_adam_clip')
 
 
 def load():
@@ -27,6 +28,11 @@ def load():
         L.d1_step.argtypes = [p, i, i, p, p, p, p, p, p, p, p]
         L.d1_sample.argtypes = [p, i, i, i, C.c_uint64, C.c_uint32, p, p, p]
         L.d1_obs_to_bf16.argtypes = [p, p, C.c_int64, p]
+        L.d1_ppo_gather.argtypes = [p, i, p, i, p, p, p, p, p, p, p, p, p, p]
+        L.d1_ppo_loss.argtypes = [p, i, i, p, p, p, p, i, C.c_float, C.c_float, C.c_float, p, p, p]
+        L.d1_relu_bwd.argtypes = [p, p, C.c_int64, p]
+        L.d1_adam_clip.argtypes = [p, p, p, p, p, C.c_int64, p, i, C.c_float, C.c_float, C.c_float, C.c_float,
+                                   C.c_float, p, p]
         L.d1_gae.argtypes = [p, p, p, p, i, i, C.c_float, C.c_float, p, p, p]
         _LIB = L
     return _LIB

@@ -51,7 +51,10 @@ class Env:
                                     self.stream), 'd1_init')
         return self.obs
 
-    def step(self, actions, active=None):
+    def step(self, actions, active=None, obs=None):
+        """`obs` optionally redirects this step's observation into another uint8
+        [batch, 15, 15, 8]-shaped buffer (e.g. a rollout-buffer slice); self.obs then
+        keeps the previous step's values."""
         if not (actions.device == self.device and actions.dtype == torch.int64 and actions.is_contiguous()
                 and actions.shape == (self.batch,)):
             raise ValueError('actions must be a contiguous int64 tensor of shape [batch] on the env device')
@@ -61,7 +64,13 @@ class Env:
                     and active.shape == (self.batch,)):
                 raise ValueError('active must be a contiguous bool tensor of shape [batch] on the env device')
             act = active.data_ptr()
+        dst = self.obs
+        if obs is not None:
+            if not (obs.device == self.device and obs.dtype == torch.uint8 and obs.is_contiguous()
+                    and obs.numel() == self.batch * 1800):
+                raise ValueError('obs must be a contiguous uint8 buffer of batch*1800 bytes on the env device')
+            dst = obs
         _lib.check(self.lib.d1_step(self.state.data_ptr(), self.batch, self.max_monsters, C.byref(self.cfg),
-                                    C.byref(self.tables), actions.data_ptr(), self.obs.data_ptr(),
+                                    C.byref(self.tables), actions.data_ptr(), dst.data_ptr(),
                                     self.out.data_ptr(), self.hash.data_ptr(), act, self.stream), 'd1_step')
-        return self.obs, self.out
+        return dst, self.out

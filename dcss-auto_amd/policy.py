@@ -31,7 +31,10 @@ class Policy(nn.Module):
 
     def forward(self, obs_u8):
         """obs uint8 [B, 15, 15, 8] (or [B, 1800]) -> (fp32 logits [B, A], fp32 value [B])."""
-        x = widen(obs_u8.reshape(obs_u8.shape[0], -1), self.l1.weight.dtype)
+        dtype = self.l1.weight.dtype
+        if obs_u8.is_cuda and torch.is_autocast_enabled('cuda'):
+            dtype = torch.get_autocast_dtype('cuda')
+        x = widen(obs_u8.reshape(obs_u8.shape[0], -1), dtype)
         if x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_grad_enabled():
             # bias + ReLU in the hipBLASLt epilogue
             h = torch._addmm_activation(self.l1.bias, x, self.l1.weight.t())

@@ -117,6 +117,27 @@ int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t
  * count must be a multiple of 16 and both pointers 16-byte aligned. */
 int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stream);
 
+/* PPO minibatch pieces (graph-safe: no memsets, no cross-workgroup atomics).
+ * d1_ppo_gather: rows idx[mb] of uint8 obs [*, row_bytes] -> bf16 xb [mb, row_bytes] and the
+ *   per-sample action (int32), old log-prob, advantage and return.
+ * d1_ppo_loss: clipped surrogate + vcoef*0.5*(v-R)^2 - ecoef*H on bf16 head outputs
+ *   z [mb, ldz] = [k logits | value]; writes dL/dz (bf16, same layout) and per-workgroup
+ *   partial sums (pg, value, entropy) to partial[4*ceil(mb/256)]
+ *   (loss of gpu-d1/scripts/run_ring_ablations.py:364-367).
+ * d1_relu_bwd: dh *= (h > 0) on bf16 buffers of n elements.
+ * d1_adam_clip: global-norm clipping (max_norm) + Adam over flat fp32 params p (bf16 copy pb
+ *   refreshed), bf16 grads g, fp32 moments m/v; partial holds nparts floats of scratch;
+ *   step[0..1] is the device-side step counter (torch.optim.Adam semantics, no decay). */
+int d1_ppo_gather(const uint8_t *obs, int row_bytes, const int64_t *idx, int mb, const int64_t *act,
+                  const float *logp, const float *adv, const float *ret, void *xb, int32_t *act_o,
+                  float *logp_o, float *adv_o, float *ret_o, void *stream);
+int d1_ppo_loss(const void *z, int ldz, int k, const int32_t *act, const float *old_logp, const float *adv,
+                const float *ret, int mb, float clip, float vcoef, float ecoef, void *dz, float *partial,
+                void *stream);
+int d1_relu_bwd(void *dh, const void *h, int64_t n, void *stream);
+int d1_adam_clip(float *p, void *pb, const void *g, float *m, float *v, int64_t n, float *partial, int nparts,
+                 float max_norm, float lr, float b1, float b2, float eps, float *step, void *stream);
+
 /* Reverse-time GAE over a [T, n] rollout (gpu-d1/scripts/run_ring_ablations.py:354-360):
  *   live = 1 - done[t]; delta = reward[t] + (gamma*next)*live - value[t];
  *   gae = delta + (gamma_lambda*live)*gae; adv[t] = gae; next = value[t]

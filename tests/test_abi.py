@@ -15,7 +15,8 @@ def declared_symbols():
 def test_header_declares_the_abi():
     assert declared_symbols() == sorted(['d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size',
                                          'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_gae',
-                                         'd1_obs_to_bf16'])
+                                         'd1_obs_to_bf16', 'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd',
+                                         'd1_adam_clip'])
 
 
 def test_library_exports_declared_symbols(pkg):

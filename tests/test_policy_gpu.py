@@ -120,3 +120,153 @@ def test_policy_forward_matches_fp32_reference():
         out = h @ w['head.weight'].t() + w['head.bias']
     torch.testing.assert_close(logits, out[:, :16], rtol=2e-2, atol=2e-2)
     torch.testing.assert_close(value, out[:, 16], rtol=2e-2, atol=2e-2)
+
+
+def reference_loss(logits, values, actions, old_logp, adv, ret, clip=0.2):
+    """The reference's loss expression (gpu-d1/scripts/run_ring_ablations.py:365-367) with
+    C4's coefficients (value 0.5 x 0.5*MSE = the reference's .25*MSE, entropy 0.01)."""
+    from torch.distributions import Categorical
+    dist = Categorical(logits=logits)
+    ratio = (dist.log_prob(actions) - old_logp).exp()
+    pg = -torch.minimum(ratio * adv, ratio.clamp(1 - clip, 1 + clip) * adv).mean()
+    return pg + .25 * (values - ret).square().mean() - 0.01 * dist.entropy().mean()
+
+
+def test_ppo_loss_matches_reference_fp32():
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    g = torch.Generator().manual_seed(5)
+    n = 8192
+    logits = torch.randn(n, 16, generator=g) * 3
+    values = torch.randn(n, generator=g)
+    actions = torch.randint(0, 16, (n,), generator=g)
+    old = torch.log_softmax(logits + 0.3 * torch.randn(n, 16, generator=g), 1).gather(1, actions[:, None]).squeeze(1)
+    adv = torch.randn(n, generator=g)
+    ret = torch.randn(n, generator=g)
+    want = reference_loss(logits.double(), values.double(), actions, old.double(), adv.double(), ret.double())
+    got, *_ = ppo.ppo_loss(logits.cuda(), values.cuda(), actions.cuda(), old.cuda(), adv.cuda(), ret.cuda())
+    torch.testing.assert_close(got.double().cpu(), want, rtol=1e-5, atol=1e-6)
+
+
+def test_ppo_update_runs_and_improves_surrogate():
+    """One bf16-autocast PPO update on a small buffer: finite, weights move, the clipped
+    objective on the same data goes down."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    torch.manual_seed(0)
+    T, N = 8, 2048
+    buf = ppo.RolloutBuffer(T, N)
+    buf.obs.random_(0, 20)
+    model = P.Policy(seed=1).cuda()
+    with torch.no_grad():
+        logits, v = model(buf.obs.view(T * N, -1).to(torch.float32))
+    buf.actions.copy_(torch.randint(0, 16, (T, N), device='cuda'))
+    buf.logp.copy_(torch.log_softmax(logits, 1).gather(1, buf.actions.view(-1, 1)).view(T, N))
+    buf.values.copy_(v.view(T, N))
+    buf.rewards.copy_(torch.where(torch.rand(T, N, device='cuda') < 0.5, 1.0, -1.0) * (buf.actions == 3))
+    trainer = ppo.PPO(model, epochs=2, minibatch=4096)
+    before = [p.detach().clone() for p in model.parameters()]
+    loss = trainer.update(buf)
+    assert torch.isfinite(loss)
+    assert any(not torch.equal(a, b) for a, b in zip(before, model.parameters()))
+
+
+def test_graphed_ppo_matches_eager_every_replay():
+    """The captured minibatch step must reproduce eager stepping on every replay, with
+    eager work and synchronisations between replays (HIP-graph replay check)."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    T, N, mb = 4, 4096, 4096
+    buf = ppo.RolloutBuffer(T, N)
+    torch.manual_seed(3)
+    buf.obs.random_(0, 20)
+    buf.actions.random_(0, 16)
+    buf.logp.copy_(-torch.rand(T, N, device='cuda') * 3)
+    buf.values.normal_()
+    buf.rewards.copy_(torch.randn(T, N, device='cuda') * (torch.rand(T, N, device='cuda') < 0.1))
+    buf.dones.copy_((torch.rand(T, N, device='cuda') < 0.05).to(torch.uint8))
+    eager_model, graph_model = P.Policy(seed=2).cuda(), P.Policy(seed=2).cuda()
+    eager = ppo.PPO(eager_model, epochs=1, minibatch=mb)
+    graphed = ppo.PPO(graph_model, epochs=1, minibatch=mb, graph=True)
+    graphed._capture(buf)
+    adv, ret = eager.advantages(buf)
+    graphed._adv.copy_(adv)
+    graphed._ret.copy_(ret)
+    n = T * N
+    obs, act, logp = buf.obs.view(n, -1), buf.actions.view(n), buf.logp.view(n)
+    for r in range(6):
+        inds = torch.randperm(n, device='cuda')[:mb]
+        eager.minibatch_step(obs.index_select(0, inds), act[inds], logp[inds], adv[inds], ret[inds])
+        graphed._idx.copy_(inds)
+        graphed._g.replay()
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device='cuda').sum().item()      # unrelated eager work between replays
+        for (name, a), b in zip(eager_model.named_parameters(), graph_model.parameters()):
+            torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-6, msg=f'replay {r} {name}')
+
+
+def _small_buffer(T, N, seed=3):
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    buf = ppo.RolloutBuffer(T, N)
+    torch.manual_seed(seed)
+    buf.obs.random_(0, 20)
+    buf.actions.random_(0, 16)
+    buf.logp.copy_(-torch.rand(T, N, device='cuda') * 3)
+    buf.values.normal_()
+    buf.rewards.copy_(torch.randn(T, N, device='cuda') * (torch.rand(T, N, device='cuda') < 0.1))
+    buf.dones.copy_((torch.rand(T, N, device='cuda') < 0.05).to(torch.uint8))
+    buf.bootstrap.normal_()
+    return buf
+
+
+def test_fast_ppo_gradients_match_autograd():
+    """Explicit backward (libd1hip loss/ReLU kernels + GEMMs) vs torch autograd under bf16
+    autocast on the same minibatch: gradients within the bf16 bar (2e-2 relative to the
+    gradient scale), loss terms within 1e-5 of the fp32 formula on the same head outputs."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    T, N, mb = 2, 4096, 8192
+    buf = _small_buffer(T, N)
+    model = P.Policy(seed=4).cuda()
+    fast = ppo.FastPPO(model, minibatch=mb, graph=False, max_grad_norm=1e9)
+    adv, ret = fast.advantages(buf)
+    obs, actions, logp = fast._views(buf)
+    fast.idx.copy_(torch.arange(mb, device='cuda'))
+    fast._step(obs, actions, logp, adv, ret)
+    x = obs[:mb]
+    with torch.autocast('cuda', dtype=torch.bfloat16):
+        logits, value = model(x)
+    loss, pg, vl, ent = ppo.ppo_loss(logits, value, actions[:mb], logp[:mb], adv[:mb], ret[:mb])
+    loss.backward()
+    terms = fast.loss_terms()
+    torch.testing.assert_close(terms, torch.stack([pg, vl, ent]).float(), rtol=2e-2, atol=1e-4)
+    for name, prm in model.named_parameters():
+        g = fast.flat.view(fast.flat.g, name).float()
+        scale = prm.grad.abs().max().item() + 1e-12
+        err = (g - prm.grad).abs().max().item() / scale
+        assert err < 2e-2, (name, err)
+
+
+def test_fast_ppo_graph_replays_match_eager():
+    """Captured vs eager minibatch steps, with eager torch reductions between replays: the
+    flat parameters must agree bit for bit after every replay."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    T, N, mb = 4, 4096, 4096
+    buf = _small_buffer(T, N)
+    eager = ppo.FastPPO(P.Policy(seed=2).cuda(), minibatch=mb, graph=False)
+    graphed = ppo.FastPPO(P.Policy(seed=2).cuda(), minibatch=mb, graph=True)
+    graphed._capture(buf)
+    adv, ret = eager.advantages(buf)
+    graphed._adv.copy_(adv)
+    graphed._ret.copy_(ret)
+    obs, actions, logp = eager._views(buf)
+    for r in range(8):
+        inds = torch.randperm(T * N, device='cuda')[:mb]
+        eager.idx.copy_(inds)
+        eager._step(obs, actions, logp, adv, ret)
+        graphed.idx.copy_(inds)
+        graphed._g.replay()
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device='cuda').sum().item()      # eager reductions between replays
+        assert torch.equal(eager.flat.p, graphed.flat.p), f'replay {r}'
+        assert torch.equal(eager.step_t, graphed.step_t)
