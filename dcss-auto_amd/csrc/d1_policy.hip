@@ -200,6 +200,76 @@ __global__ __launch_bounds__(256) void k_relu_bwd(uint16_t *__restrict__ dh, con
     if (i < n && !(bf16_to_f(h[i]) > 0.f)) dh[i] = 0;
 }
 
+// ReLU backward fused with the bias gradient: dh *= (h > 0) on a [rows, cols] bf16 block
+// (cols <= 256), and colpart[b*cols + c] = sum over this workgroup's rows of the masked dh.
+// Workgroup = 256 lanes, lane = column; rows split in chunks of `rows_per`.
+__global__ __launch_bounds__(256) void k_relu_bwd_bias(uint16_t *__restrict__ dh, const uint16_t *__restrict__ h,
+                                                       int rows, int cols, int rows_per, float *__restrict__ colpart) {
+    int c = threadIdx.x;
+    int r0 = blockIdx.x * rows_per, r1 = min(rows, r0 + rows_per);
+    float acc = 0.f;
+    if (c < cols) {
+        for (int r = r0; r < r1; r++) {
+            size_t o = (size_t)r * cols + c;
+            float v = bf16_to_f(dh[o]);
+            if (!(bf16_to_f(h[o]) > 0.f)) { v = 0.f; dh[o] = 0; }
+            acc += v;
+        }
+        colpart[(size_t)blockIdx.x * cols + c] = acc;
+    }
+}
+// Column sums of a [rows, cols] bf16 block into colpart (no masking).
+__global__ __launch_bounds__(256) void k_colsum(const uint16_t *__restrict__ x, int rows, int cols, int ld,
+                                                int rows_per, float *__restrict__ colpart) {
+    int c = threadIdx.x;
+    int r0 = blockIdx.x * rows_per, r1 = min(rows, r0 + rows_per);
+    if (c < cols) {
+        float acc = 0.f;
+        for (int r = r0; r < r1; r++) acc += bf16_to_f(x[(size_t)r * ld + c]);
+        colpart[(size_t)blockIdx.x * cols + c] = acc;
+    }
+}
+// out[c] = bf16(sum_b colpart[b*cols + c]); one workgroup per column, tree sum in LDS.
+__global__ __launch_bounds__(256) void k_colsum_finish(const float *__restrict__ colpart, int nblocks, int cols,
+                                                       uint16_t *__restrict__ out) {
+    __shared__ float red[256];
+    int c = blockIdx.x;
+    float acc = 0.f;
+    for (int b = threadIdx.x; b < nblocks; b += blockDim.x) acc += colpart[(size_t)b * cols + c];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = blockDim.x / 2; o; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[c] = f_to_bf16(red[0]);
+}
+// out[j] = bf16(sum_s part[s*n + j]) over S split-K partials (bf16), 8 elements per lane.
+__global__ __launch_bounds__(256) void k_sum_partials(const uint16_t *__restrict__ part, int S, size_t n,
+                                                      uint16_t *__restrict__ out) {
+    size_t j = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (j >= n) return;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (j + 8 <= n && (n % 8) == 0) {
+        for (int q = 0; q < S; q++) {
+            uint4 v = *(const uint4 *)(part + (size_t)q * n + j);
+            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) { acc[2 * e] += bf16_to_f((uint16_t)w[e]); acc[2 * e + 1] += bf16_to_f((uint16_t)(w[e] >> 16)); }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (uint32_t)f_to_bf16(acc[2 * e]) | ((uint32_t)f_to_bf16(acc[2 * e + 1]) << 16);
+        *(uint4 *)(out + j) = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+        for (size_t k = j; k < n && k < j + 8; k++) {
+            float a = 0.f;
+            for (int q = 0; q < S; q++) a += bf16_to_f(part[(size_t)q * n + k]);
+            out[k] = f_to_bf16(a);
+        }
+    }
+}
+
 // Sum of squares of the bf16 gradient buffer: one partial per workgroup.
 __global__ __launch_bounds__(256) void k_sqnorm(const uint16_t *__restrict__ g, size_t n, float *__restrict__ partial,
                                                 float *__restrict__ step) {
@@ -303,6 +373,32 @@ int d1_relu_bwd(void *dh, const void *h, int64_t n, void *stream) {
     if (n == 0) return 0;
     hipLaunchKernelGGL(d1p::k_relu_bwd, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        (uint16_t *)dh, (const uint16_t *)h, (size_t)n);
+    return (int)hipGetLastError();
+}
+int d1_relu_bwd_bias(void *dh, const void *h, int rows, int cols, float *colpart, int nblocks, void *bias_grad,
+                     void *stream) {
+    if (rows <= 0 || cols <= 0 || cols > 256 || nblocks < 1 || !dh || !h || !colpart || !bias_grad) return D1_E_ARG;
+    int per = (rows + nblocks - 1) / nblocks;
+    hipLaunchKernelGGL(d1p::k_relu_bwd_bias, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, (uint16_t *)dh,
+                       (const uint16_t *)h, rows, cols, per, colpart);
+    hipLaunchKernelGGL(d1p::k_colsum_finish, dim3(cols), dim3(256), 0, (hipStream_t)stream, colpart, nblocks, cols,
+                       (uint16_t *)bias_grad);
+    return (int)hipGetLastError();
+}
+int d1_colsum(const void *x, int rows, int cols, int ld, float *colpart, int nblocks, void *out, void *stream) {
+    if (rows <= 0 || cols <= 0 || cols > 256 || ld < cols || nblocks < 1 || !x || !colpart || !out) return D1_E_ARG;
+    int per = (rows + nblocks - 1) / nblocks;
+    hipLaunchKernelGGL(d1p::k_colsum, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, rows,
+                       cols, ld, per, colpart);
+    hipLaunchKernelGGL(d1p::k_colsum_finish, dim3(cols), dim3(256), 0, (hipStream_t)stream, colpart, nblocks, cols,
+                       (uint16_t *)out);
+    return (int)hipGetLastError();
+}
+int d1_sum_partials(const void *part, int S, int64_t n, void *out, void *stream) {
+    if (S < 1 || n <= 0 || !part || !out) return D1_E_ARG;
+    size_t threads = ((size_t)n + 7) / 8;
+    hipLaunchKernelGGL(d1p::k_sum_partials, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)part, S, (size_t)n, (uint16_t *)out);
     return (int)hipGetLastError();
 }
 int d1_adam_clip(float *p, void *pb, const void *g, float *m, float *v, int64_t n, float *partial, int nparts,

@@ -197,7 +197,10 @@ class FastPPO:
         self.adv_mb = torch.empty(mb, dtype=torch.float32, device=dev)
         self.ret_mb = torch.empty(mb, dtype=torch.float32, device=dev)
         self.dz = torch.empty((mb, 17), dtype=torch.bfloat16, device=dev)
-        self.ones = torch.ones((mb, 1), dtype=torch.bfloat16, device=dev)
+        self.colblocks = 512
+        self.colpart = torch.zeros(self.colblocks * 256, dtype=torch.float32, device=dev)
+        self.splitk = 16 if mb % 16 == 0 else 1
+        self.kpart = torch.empty(self.splitk * 256 * OBS, dtype=torch.bfloat16, device=dev)
         self._g = self._g_buf = None
 
     # one minibatch whose indices are in self.idx; buffers are flattened [T*N, ...] views
@@ -219,19 +222,35 @@ class FastPPO:
                                  self.adv_mb.data_ptr(), self.ret_mb.data_ptr(), mb, self.clip, self.vcoef, self.ecoef,
                                  self.dz.data_ptr(), self.loss_parts.data_ptr(), s), 'd1_ppo_loss')
         G = lambda name: F.view(F.g, name)   # noqa: E731
-        torch.mm(self.dz.t(), h2, out=G('head.weight'))
-        torch.mm(self.dz.t(), self.ones, out=G('head.bias').view(17, 1))
+        cb, cp = self.colblocks, self.colpart.data_ptr()
+        self._wgrad(self.dz, h2, G('head.weight'))
+        _lib.check(L.d1_colsum(self.dz.data_ptr(), mb, 17, 17, cp, cb, G('head.bias').data_ptr(), s), 'd1_colsum')
         dh2 = torch.mm(self.dz, W3)
-        _lib.check(L.d1_relu_bwd(dh2.data_ptr(), h2.data_ptr(), dh2.numel(), s), 'd1_relu_bwd')
-        torch.mm(dh2.t(), h1, out=G('l2.weight'))
-        torch.mm(dh2.t(), self.ones, out=G('l2.bias').view(256, 1))
+        _lib.check(L.d1_relu_bwd_bias(dh2.data_ptr(), h2.data_ptr(), mb, 256, cp, cb, G('l2.bias').data_ptr(), s),
+                   'd1_relu_bwd_bias')
+        self._wgrad(dh2, h1, G('l2.weight'))
         dh1 = torch.mm(dh2, W2)
-        _lib.check(L.d1_relu_bwd(dh1.data_ptr(), h1.data_ptr(), dh1.numel(), s), 'd1_relu_bwd')
-        torch.mm(dh1.t(), self.xb, out=G('l1.weight'))
-        torch.mm(dh1.t(), self.ones, out=G('l1.bias').view(256, 1))
+        _lib.check(L.d1_relu_bwd_bias(dh1.data_ptr(), h1.data_ptr(), mb, 256, cp, cb, G('l1.bias').data_ptr(), s),
+                   'd1_relu_bwd_bias')
+        self._wgrad(dh1, self.xb, G('l1.weight'))
         _lib.check(L.d1_adam_clip(F.p.data_ptr(), F.pb.data_ptr(), F.g.data_ptr(), F.m.data_ptr(), F.v.data_ptr(),
                                   F.n, self.norm_parts.data_ptr(), self.nparts, self.max_grad_norm, self.lr, 0.9,
                                   0.999, self.eps, self.step_t.data_ptr(), s), 'd1_adam_clip')
+
+    def _wgrad(self, dy, x, out):
+        """out = dy^T @ x with the batch (K) dimension split S ways: one bf16 bmm into
+        [S, M, N] partials (right operand contiguous), then a libd1hip partial sum."""
+        from . import _lib
+        S = self.splitk
+        if S == 1:
+            torch.mm(dy.t(), x, out=out)
+            return
+        mb, M = dy.shape
+        N = x.shape[1]
+        part = self.kpart[:S * M * N].view(S, M, N)
+        torch.bmm(dy.view(S, mb // S, M).transpose(1, 2), x.view(S, mb // S, N), out=part)
+        _lib.check(_lib.load().d1_sum_partials(part.data_ptr(), S, M * N, out.data_ptr(),
+                                               torch.cuda.current_stream(self.dev).cuda_stream), 'd1_sum_partials')
 
     def loss_terms(self):
         """(pg, value, entropy) means of the last minibatch (reads device partials)."""

@@ -135,6 +135,15 @@ int d1_ppo_loss(const void *z, int ldz, int k, const int32_t *act, const float *
                 const float *ret, int mb, float clip, float vcoef, float ecoef, void *dz, float *partial,
                 void *stream);
 int d1_relu_bwd(void *dh, const void *h, int64_t n, void *stream);
+/* ReLU backward fused with the bias gradient of a [rows, cols<=256] bf16 block:
+ * dh *= (h > 0) and bias_grad[c] = sum_r dh[r, c] (bf16), via nblocks partial rows in
+ * colpart[nblocks*cols]; d1_colsum is the same column sum without the mask (row stride ld). */
+int d1_relu_bwd_bias(void *dh, const void *h, int rows, int cols, float *colpart, int nblocks, void *bias_grad,
+                     void *stream);
+int d1_colsum(const void *x, int rows, int cols, int ld, float *colpart, int nblocks, void *out, void *stream);
+/* out[j] = sum over s < S of part[s*n + j] (bf16 in, fp32 sum, bf16 out): the reduction
+ * step of a split-K GEMM. */
+int d1_sum_partials(const void *part, int S, int64_t n, void *out, void *stream);
 int d1_adam_clip(float *p, void *pb, const void *g, float *m, float *v, int64_t n, float *partial, int nparts,
                  float max_norm, float lr, float b1, float b2, float eps, float *step, void *stream);
 
