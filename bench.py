@@ -108,6 +108,31 @@ def ppo_bench(args, env, rollout_model, policy_mod, dev):
                      'frac': flops / dt / 1e12 / BF16_PEAK_TFLOPS}}
 
 
+REFERENCE_WAITS_PER_S = 10.165e6   # gpu-d1/RESULTS.md:16, warp per world, RTX 5000 Max-Q
+
+
+def wait_bench(args, worlds=8192, count=8, chunk=64, waits=4096):
+    """The reference's sustained wait comparison (gpu-d1/RESULTS.md:5-16): 8,192 worlds,
+    8 monsters, mixed approach/contact phases, 64 waits per kernel, 4,096 waits per world."""
+    import torch
+    wait = importlib.import_module('dcss-auto_amd.wait')
+    w = wait.WaitWorlds(worlds, count, 'mixed', seed=42)
+    w.run(chunk)                       # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(waits // chunk):
+        w.run(chunk)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    rate = worlds * waits / dt
+    return {'metric': 'monster waits/s (reference wait benchmark, 8,192 worlds, 8 monsters, mixed)',
+            'value': rate, 'unit': 'waits/s', 'n_gpus': 1, 'higher_is_better': True,
+            'vs_baseline': rate / REFERENCE_WAITS_PER_S,
+            'baseline': {'value': REFERENCE_WAITS_PER_S, 'source': 'gpu-d1/RESULTS.md:16', 'hardware': 'Quadro RTX 5000 Max-Q'},
+            'config': {'workload': 'wait', 'worlds': worlds, 'monsters': count, 'scenario': 'mixed',
+                       'waits_per_kernel': chunk, 'waits_per_world': waits}, 'seconds': dt}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -116,7 +141,7 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo'], default='rollout',
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'wait'], default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
                          'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer')
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
@@ -127,6 +152,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.mode == 'wait':
+        print(json.dumps(wait_bench(args)), flush=True)
+        return
     pkg = importlib.import_module('dcss-auto_amd')
     policy_mod = importlib.import_module('dcss-auto_amd.policy')
     dev = torch.device('cuda:0')

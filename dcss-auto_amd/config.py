@@ -42,6 +42,10 @@ class D1Tables(C.Structure):
     _fields_ = [('floor', C.c_void_p), ('cells', C.c_void_p), ('ray_slots', C.c_void_p), ('nslots', C.c_int32)]
 
 
+class D1WaitMap(C.Structure):
+    _fields_ = [('floor', C.c_void_p), ('dist', C.c_void_p), ('starts', C.c_void_p), ('player', C.c_int32)]
+
+
 RNG_PCG, RNG_COUNTER = 0, 1
 LEVEL_SHARED, LEVEL_GENERATED = 0, 1
 

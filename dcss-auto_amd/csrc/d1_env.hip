@@ -411,6 +411,13 @@ __device__ __forceinline__ void occ_set(Ctx &x, int p, bool on) {
     __syncthreads();
 }
 
+__device__ __forceinline__ void occ_set_lane(Ctx &x, int p) {
+    atomicOr(&x.sm->occ[(p / W) * RW + ((p % W) >> 5)], 1u << ((p % W) & 31));
+}
+__device__ __forceinline__ void occ_clear_lane(Ctx &x, int p) {
+    atomicAnd(&x.sm->occ[(p / W) * RW + ((p % W) >> 5)], ~(1u << ((p % W) & 31)));
+}
+
 // ---------------------------------------------------------------- cell selection
 // Row prefix counts of a bitmap (rows in `bm`), stored inclusive in sm->rowpre.
 __device__ __forceinline__ int row_prefix(Ctx &x, const uint32_t *bm) {
@@ -986,6 +993,142 @@ __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, s
     if (hash && x.lane == 0) hash[env] = h;
 }
 
+// ---------------------------------------------------------------- monster-wait workload
+// The reference's wait benchmark (gpu-d1/src/bench.cu:36-96,151-184 over
+// gpu-d1/src/sim.h:93-122,276-295): a stationary player on a fixed map, `count` awake
+// monsters at a fixture spawn list, a static distance-from-player field; one call runs
+// `steps` waits per world. World row (WAIT_BYTES): header then {i16 pos, i16 energy} x 64.
+constexpr int WAIT_BYTES = 64 + 4 * 64;
+struct WaitHdr {
+    uint64_t rng_state, rng_inc;
+    int32_t hp, regen, blocks, fixture, episode;
+    int32_t pad[7];
+};
+static_assert(sizeof(WaitHdr) == 64, "wait header");
+
+__device__ __forceinline__ void wait_stage_map(Ctx &x, const D1WaitMap &map) {
+    Smem *sm = x.sm;
+    for (int s = 0; s < 2; s++) {
+        int y = x.lane + 64 * s;
+        if (y >= H) break;
+        for (int j = 0; j < 3; j++) {
+            uint32_t f = 0, r = 0;
+            for (int b = 0; b < 32 && 32 * j + b < W; b++) {
+                int p = y * W + 32 * j + b;
+                f |= (uint32_t)(map.floor[p] != 0) << b;
+                r |= (uint32_t)(map.dist[p] != 65535) << b;
+            }
+            sm->floor[y * RW + j] = f;
+            sm->reach[y * RW + j] = r;
+            sm->occ[y * RW + j] = 0;
+        }
+    }
+    for (int p = x.lane; p < N; p += 64) sm->dist[p] = (uint8_t)map.dist[p];
+    __syncthreads();
+}
+// gpu-d1/src/sim.h:93-111
+__device__ __forceinline__ void wait_reset(Ctx &x, const D1WaitMap &map, int count, int fixture, bool first) {
+    if (!first && x.lane < count) occ_clear_lane(x, x.mpos);
+    __syncthreads();
+    x.hp = x.c->hp; x.regen = 0; x.blocks = 0;
+    for (int i = 0; i < count; i++) {
+        int p = map.starts[fixture * 64 + i];
+        int en = 70 + x.g.r(10);
+        if (x.lane == i) { x.mpos = p; x.menergy = en; }
+    }
+    if (x.lane < count) occ_set_lane(x, x.mpos);
+    __syncthreads();
+    if (!first) x.episode++;
+}
+// gpu-d1/src/sim.h:112-122,276-295 (scan scheduler; the heap picks the same actors)
+__device__ __forceinline__ void wait_step(Ctx &x, const D1WaitMap &map, int count, int fixture) {
+    if (x.hp <= 0) wait_reset(x, map, count, fixture, false);
+    x.blocks = 0;
+    x.regen += x.c->regen;
+    while (x.regen >= 100) { x.hp = imin(x.c->hp, x.hp + 1); x.regen -= 100; }
+    bool mine = x.lane < count;
+    if (mine) x.menergy = (int16_t)(x.menergy + kind_speed(x.c, x.mkind));
+    while (x.hp > 0) {
+        int key = (mine && x.menergy >= 80) ? x.menergy * 128 + 127 - x.lane : -1;
+        key = wave_max(key);
+        if (key < 0) break;
+        act(x, 127 - (key & 127));
+    }
+}
+__device__ __forceinline__ uint32_t wait_digest(Ctx &x, int count) {
+    uint32_t h = x.lane < count ? term((uint16_t)x.mpos | (uint32_t)(uint16_t)x.menergy << 16, 100 + x.lane) : 0u;
+    h = wave_sum(h);
+    return h + term((uint32_t)x.hp, 0) + term((uint32_t)x.regen, 1) + term((uint32_t)x.blocks, 2) +
+           term((uint32_t)x.episode, 3) + term((uint32_t)x.g.st, 4) + term((uint32_t)(x.g.st >> 32), 5);
+}
+__device__ __forceinline__ void wait_load(Ctx &x, const uint8_t *row, int count, int &fixture) {
+    WaitHdr h = *(const WaitHdr *)row;
+    x.g.mode = 0; x.g.st = h.rng_state; x.g.inc = h.rng_inc;
+    x.hp = h.hp; x.regen = h.regen; x.blocks = h.blocks; x.episode = h.episode; fixture = h.fixture;
+    x.mpos = -1; x.menergy = -30000; x.mkind = x.lane % 6; x.mhp = 1; x.mawake = 1;
+    if (x.lane < count) {
+        const int16_t *m = (const int16_t *)(row + 64) + 2 * x.lane;
+        x.mpos = m[0]; x.menergy = m[1];
+        occ_set_lane(x, x.mpos);
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ void wait_store(Ctx &x, uint8_t *row, int count, int fixture) {
+    if (x.lane == 0) {
+        WaitHdr h{};
+        h.rng_state = x.g.st; h.rng_inc = x.g.inc;
+        h.hp = x.hp; h.regen = x.regen; h.blocks = x.blocks; h.fixture = fixture; h.episode = x.episode;
+        *(WaitHdr *)row = h;
+    }
+    if (x.lane < count) {
+        int16_t *m = (int16_t *)(row + 64) + 2 * x.lane;
+        m[0] = (int16_t)x.mpos; m[1] = (int16_t)x.menergy;
+    }
+}
+__device__ __forceinline__ void wait_ctx(Ctx &x, Smem *sm, const D1Config *cfg, const D1WaitMap &map) {
+    x.sm = sm; x.c = cfg; x.rays = nullptr; x.nslots = 0; x.lane = lane_id(); x.adj_clear = true;
+    x.player = map.player; x.vis0 = x.vis1 = x.vis2 = x.vis3 = 0;
+}
+// scenario 0 contact, 1 approach, 2 mixed (fixture = world % 2, then (world*7)%32 warm-up
+// waits), as gpu-d1/src/bench.cu:151-166.
+__global__ __launch_bounds__(64) void k_wait_init(uint8_t *worlds, int n, int count, D1Config cfg, D1WaitMap map,
+                                                  uint64_t seed, int scenario) {
+    __shared__ Smem sm;
+    int w = blockIdx.x;
+    if (w >= n) return;
+    Ctx x;
+    wait_ctx(x, &sm, &cfg, map);
+    wait_stage_map(x, map);
+    x.g.pcg_seed(mix64(seed + (uint64_t)w), (uint64_t)w + 1);
+    int fixture = scenario == 1 ? 1 : scenario == 2 ? w % 2 : 0;
+    x.episode = 0;
+    x.mpos = -1; x.menergy = -30000; x.mkind = x.lane % 6; x.mhp = 1; x.mawake = 1;
+    wait_reset(x, map, count, fixture, true);
+    int warm = scenario == 2 ? (w * 7) % 32 : 0;
+    for (int k = 0; k < warm; k++) wait_step(x, map, count, fixture);
+    wait_store(x, worlds + (size_t)w * WAIT_BYTES, count, fixture);
+}
+__global__ __launch_bounds__(64) void k_wait(uint8_t *worlds, int n, int count, D1Config cfg, D1WaitMap map, int steps,
+                                             uint32_t *trace) {
+    __shared__ Smem sm;
+    int w = blockIdx.x;
+    if (w >= n) return;
+    Ctx x;
+    wait_ctx(x, &sm, &cfg, map);
+    wait_stage_map(x, map);
+    int fixture = 0;
+    uint8_t *row = worlds + (size_t)w * WAIT_BYTES;
+    wait_load(x, row, count, fixture);
+    for (int k = 0; k < steps; k++) {
+        wait_step(x, map, count, fixture);
+        if (trace) {
+            uint32_t h = wait_digest(x, count);
+            if (x.lane == 0) trace[(size_t)w * steps + k] = h;
+        }
+    }
+    wait_store(x, row, count, fixture);
+}
+
 int validate(int n, int max_m, const D1Config *c, const D1Tables *t) {
     if (n < 0 || max_m < 1 || max_m > D1_MAX_MONSTERS || !c || !t || !t->ray_slots) return D1_E_ARG;
     if (t->nslots < 1 || t->nslots > 64) return D1_E_ARG;
@@ -1014,6 +1157,34 @@ int d1_action_size(void) { return D1_ACTIONS; }
 int d1_out_size(void) { return D1_OUT; }
 int d1_config_bytes(void) { return (int)sizeof(D1Config); }
 
+int d1_wait_bytes(void) { return d1::WAIT_BYTES; }
+static int wait_validate(int n, int count, const D1Config *cfg, const D1WaitMap *map) {
+    if (n < 0 || count < 0 || count > 64 || !cfg || !map || !map->floor || !map->dist || !map->starts) return D1_E_ARG;
+    if (map->player < 0 || map->player >= D1_N) return D1_E_ARG;
+    for (int k = 0; k < 6; k++)
+        if (cfg->kinds[k].speed < 0 || cfg->kinds[k].speed > 20) return D1_E_CONFIG;
+    return 0;
+}
+int d1_wait_init(void *worlds, int n, int count, const D1Config *cfg, const D1WaitMap *map, uint64_t seed,
+                 int scenario, void *stream) {
+    int e = wait_validate(n, count, cfg, map);
+    if (e) return e;
+    if (!worlds || scenario < 0 || scenario > 2) return D1_E_ARG;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(d1::k_wait_init, dim3(n), dim3(64), 0, (hipStream_t)stream, (uint8_t *)worlds, n, count,
+                       *cfg, *map, seed, scenario);
+    return (int)hipGetLastError();
+}
+int d1_wait_run(void *worlds, int n, int count, const D1Config *cfg, const D1WaitMap *map, int steps,
+                uint32_t *trace, void *stream) {
+    int e = wait_validate(n, count, cfg, map);
+    if (e) return e;
+    if (!worlds || steps < 0) return D1_E_ARG;
+    if (n == 0 || steps == 0) return 0;
+    hipLaunchKernelGGL(d1::k_wait, dim3(n), dim3(64), 0, (hipStream_t)stream, (uint8_t *)worlds, n, count, *cfg,
+                       *map, steps, trace);
+    return (int)hipGetLastError();
+}
 int d1_init(void *state, int n, int max_monsters, const D1Config *cfg, const D1Tables *tab, uint64_t seed,
             uint8_t *obs, uint32_t *hash, void *stream) {
     int e = d1::validate(n, max_monsters, cfg, tab);

@@ -104,6 +104,28 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
             const int64_t *actions, uint8_t *obs, float *out, uint32_t *hash,
             const uint8_t *active, void *stream);
 
+/* ---- the reference's monster-wait benchmark workload (gpu-d1/src/bench.cu) ----
+ * A stationary player at `player` on one map, `count` (<= 64) awake monsters spawned from
+ * starts[fixture*64 + i], the static distance-from-player field `dist` (65535 =
+ * unreachable), cfg's player stats and kinds (monster i has kind i%6; task switches are
+ * ignored). World rows are d1_wait_bytes() each. */
+typedef struct D1WaitMap {
+    const uint8_t *floor;     /* byte per cell */
+    const uint16_t *dist;     /* distance from `player` per cell */
+    const int16_t *starts;    /* [2][64] spawn cells: contact, approach */
+    int32_t player;
+} D1WaitMap;
+int d1_wait_bytes(void);
+/* Replaces State::init (gpu-d1/src/bench.cu:151-166): world w seeded with
+ * PCG seed(mix(seed+w), w+1); scenario 0 contact, 1 approach, 2 mixed (fixture w%2 and
+ * (w*7)%32 warm-up waits). */
+int d1_wait_init(void *worlds, int n, int count, const D1Config *cfg, const D1WaitMap *map, uint64_t seed,
+                 int scenario, void *stream);
+/* `steps` waits per world (sim::step, gpu-d1/src/sim.h:276-295); trace (optional) is
+ * uint32 [n, steps] world digests after each wait. */
+int d1_wait_run(void *worlds, int n, int count, const D1Config *cfg, const D1WaitMap *map, int steps,
+                uint32_t *trace, void *stream);
+
 /* Categorical sampling with the counter RNG; replaces torch.distributions.Categorical
  * sample/log_prob in the rollout (gpu-d1/scripts/run_ring_ablations.py:350-351).
  * logits: float [n, k] (row stride `ld` floats), 1 <= k <= 64. For env i the uniform
