@@ -133,6 +133,50 @@ def wait_bench(args, worlds=8192, count=8, chunk=64, waits=4096):
                        'waits_per_kernel': chunk, 'waits_per_world': waits}, 'seconds': dt}
 
 
+def stress_bench(args, envs=262144, horizon=256, warmup=4):
+    """C5: 262,144 generated-level worlds with 40 monsters (HP U[40,60], half awake at
+    spawn), the bf16 trunk with the autoregressive verb(8) x target(25) head and the HIP
+    two-stage sampler, 256 steps. Reports decisions/s and k_step's algorithmic HBM rate."""
+    import torch
+    pkg = importlib.import_module('dcss-auto_amd')
+    P = importlib.import_module('dcss-auto_amd.policy')
+    dev = torch.device('cuda:0')
+    env = pkg.Env(envs, pkg.stress_config(), seed=3)
+    model = P.ARPolicy(seed=0).to(dev).to(torch.bfloat16)
+    actions = torch.zeros(envs, dtype=torch.int64, device=dev)
+
+    def one(t, ev=None):
+        if ev is not None:
+            ev[0].record()
+        env.step(actions)
+        if ev is not None:
+            ev[1].record()
+        with torch.no_grad():
+            vl, tl, _ = model(env.obs)
+        _, _, a, _ = P.sample_ar(vl, tl, 11, t)
+        actions.copy_(a)
+
+    for t in range(warmup):
+        one(t)
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(horizon)]
+    t0 = time.perf_counter()
+    for k in range(horizon):
+        one(warmup + k, events[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / horizon
+    achieved = STEP_BYTES[40] * envs / (step_ms * 1e-3) / 1e9
+    return {'metric': 'env decisions/sec at 262,144 envs, 40 monsters, AR 8x25 head (C5)',
+            'value': envs * horizon / wall, 'unit': 'decisions/s', 'n_gpus': 1, 'higher_is_better': True,
+            'ms_per_step': wall / horizon * 1e3,
+            'config': {'workload': 'C5', 'envs': envs, 'monsters': 40, 'hp': [40, 60], 'awake_pct': 50,
+                       'head': 'AR verb 8 x target 25', 'horizon': horizon},
+            'roofline': {'bound': 'hbm', 'kernel': 'd1::k_step', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
+                         'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'bytes_per_env_step': STEP_BYTES[40],
+                         'avg_launch_ms': step_ms}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -141,7 +185,7 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'wait'], default='rollout',
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'wait', 'stress'], default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
                          'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer')
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
@@ -154,6 +198,9 @@ def main():
     import torch
     if args.mode == 'wait':
         print(json.dumps(wait_bench(args)), flush=True)
+        return
+    if args.mode == 'stress':
+        print(json.dumps(stress_bench(args)), flush=True)
         return
     pkg = importlib.import_module('dcss-auto_amd')
     policy_mod = importlib.import_module('dcss-auto_amd.policy')

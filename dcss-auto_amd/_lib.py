@@ -11,7 +11,8 @@ _LIB = None
 SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
            'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16',
            'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd', 'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
-           'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run')
+           'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
+           'd1_sample_ar')
 
 
 def load():
@@ -35,6 +36,7 @@ def load():
         L.d1_relu_bwd_bias.argtypes = [p, p, i, i, p, i, p, p]
         L.d1_colsum.argtypes = [p, i, i, i, p, i, p, p]
         L.d1_sum_partials.argtypes = [p, i, C.c_int64, p, p]
+        L.d1_sample_ar.argtypes = [p, i, i, p, i, i, i, C.c_uint64, C.c_uint32, p, p, p, p, p]
         L.d1_wait_bytes.argtypes = []
         L.d1_wait_init.argtypes = [p, i, i, p, p, C.c_uint64, i, p]
         L.d1_wait_run.argtypes = [p, i, i, p, p, i, p, p]

@@ -91,3 +91,84 @@ def gae(reward, done, value, bootstrap, gamma=0.99, lam=0.95, adv=None, returns=
                         float(gamma), float(gamma * lam), adv.data_ptr(), returns.data_ptr(),
                         torch.cuda.current_stream(reward.device).cuda_stream), 'd1_gae')
     return adv, returns
+
+
+# ----------------------------------------------------------------------------------------
+# Autoregressive verb x target head (BASELINE C5), generalising the reference's
+# type-then-direction head (gpu-d1/branches/autoregressive-actions-v1/scripts/tactical_models.py:8-58):
+# verb logits from the trunk, a learned verb embedding, and a target MLP on
+# [trunk, embedding(verb)] evaluated for every verb in one pass.
+N_VERBS, N_TARGETS, EMBED, TARGET_HIDDEN = 8, 25, 16, 64
+
+
+class ARPolicy(nn.Module):
+    def __init__(self, width=256, obs=OBS, seed=0):
+        super().__init__()
+        self.l1 = nn.Linear(obs, width)
+        self.l2 = nn.Linear(width, width)
+        self.verb = nn.Linear(width, N_VERBS)
+        self.value = nn.Linear(width, 1)
+        self.embedding = nn.Parameter(torch.zeros(N_VERBS, EMBED))
+        self.t1 = nn.Linear(width + EMBED, TARGET_HIDDEN)
+        self.t2 = nn.Linear(TARGET_HIDDEN, N_TARGETS)
+        g = torch.Generator().manual_seed(seed)
+        with torch.no_grad():
+            for layer in (self.l1, self.l2, self.verb, self.value, self.t1, self.t2):
+                layer.weight.copy_(torch.randn(layer.weight.shape, generator=g) * 0.02)
+                layer.bias.zero_()
+            self.embedding.copy_(torch.randn(N_VERBS, EMBED, generator=g) * 0.1)
+
+    def forward(self, obs_u8):
+        """-> verb logits [B, 8], target logits [B, 8, 25] (one row per verb), value [B] (fp32)."""
+        dtype = self.l1.weight.dtype
+        if obs_u8.is_cuda and torch.is_autocast_enabled('cuda'):
+            dtype = torch.get_autocast_dtype('cuda')
+        x = widen(obs_u8.reshape(obs_u8.shape[0], -1), dtype)
+        h = torch.relu(self.l1(x))
+        h = torch.relu(self.l2(h))
+        w = self.t1.weight                         # [64, 256 + 16]: trunk part and embedding part
+        ht = torch.nn.functional.linear(h, w[:, :h.shape[1]], self.t1.bias)            # [B, 64]
+        ev = torch.nn.functional.linear(self.embedding.to(ht.dtype), w[:, h.shape[1]:])  # [8, 64]
+        z = torch.tanh(ht[:, None, :] + ev[None])                                       # [B, 8, 64]
+        targets = self.t2(z)                                                             # [B, 8, 25]
+        return self.verb(h).float(), targets.float(), self.value(h).float().squeeze(-1)
+
+
+class ARDistribution:
+    """p(verb) p(target | verb) with the factorised log-prob and entropy
+    (tactical_models.py:8-30): log p = log p(v) + log p(t|v); H = H(v) + sum_v p(v) H(t|v)."""
+
+    def __init__(self, verb_logits, target_logits):
+        self.lv = torch.log_softmax(verb_logits, -1)
+        self.lt = torch.log_softmax(target_logits, -1)
+
+    @property
+    def probs(self):
+        return (self.lv.exp()[:, :, None] * self.lt.exp()).flatten(1)
+
+    def log_prob(self, verb, target):
+        lt = self.lt.gather(1, verb[:, None, None].expand(-1, 1, self.lt.shape[2])).squeeze(1)
+        return self.lv.gather(1, verb[:, None]).squeeze(1) + lt.gather(1, target[:, None]).squeeze(1)
+
+    def entropy(self):
+        pv = self.lv.exp()
+        ht = -(self.lt.exp() * self.lt).sum(-1)
+        return -(pv * self.lv).sum(-1) + (pv * ht).sum(-1)
+
+
+def sample_ar(verb_logits, target_logits, seed, t):
+    """HIP two-stage sample -> (verb int32, target int32, env action int64, logp fp32)."""
+    n, nv = verb_logits.shape
+    nt = target_logits.shape[2]
+    assert verb_logits.dtype == torch.float32 and target_logits.dtype == torch.float32
+    assert verb_logits.stride(1) == 1 and target_logits.is_contiguous()
+    dev = verb_logits.device
+    verb = torch.empty(n, dtype=torch.int32, device=dev)
+    target = torch.empty(n, dtype=torch.int32, device=dev)
+    action = torch.empty(n, dtype=torch.int64, device=dev)
+    logp = torch.empty(n, dtype=torch.float32, device=dev)
+    L = _lib.load()
+    _lib.check(L.d1_sample_ar(verb_logits.data_ptr(), nv, verb_logits.stride(0), target_logits.data_ptr(), nt,
+                              nv * nt, n, seed, t & 0xFFFFFFFF, verb.data_ptr(), target.data_ptr(), action.data_ptr(),
+                              logp.data_ptr(), torch.cuda.current_stream(dev).cuda_stream), 'd1_sample_ar')
+    return verb, target, action, logp

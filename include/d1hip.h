@@ -135,6 +135,17 @@ int d1_wait_run(void *worlds, int n, int count, const D1Config *cfg, const D1Wai
 int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t t,
               int64_t *actions, float *logp, void *stream);
 
+/* Autoregressive two-stage sample (the type-then-direction head of
+ * gpu-d1/branches/autoregressive-actions-v1/scripts/tactical_models.py:8-30, generalised
+ * to nv verbs x nt targets): verb from verb_logits [n, ldv], then target from
+ * target_logits [n][nv][nt] (row stride ldt) of that verb; uniforms are Philox words 0/1
+ * of ctr={0, t, i, 3}. Writes verb, target, the env action (verb 0/1 + a Chebyshev-1
+ * target of the 5x5 grid -> MOVE d / ATTACK 8+d, other targets -1; verb 2/3/4 ->
+ * 16/17/18; verbs 5-7 -> 16) and log p(verb) + log p(target | verb). */
+int d1_sample_ar(const float *verb_logits, int nv, int ldv, const float *target_logits, int nt, int ldt, int n,
+                 uint64_t seed, uint32_t t, int32_t *verb, int32_t *target, int64_t *action, float *logp,
+                 void *stream);
+
 /* Widen `count` uint8 observation bytes to bf16 (exact), for the policy trunk.
  * count must be a multiple of 16 and both pointers 16-byte aligned. */
 int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stream);

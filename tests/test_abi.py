@@ -17,7 +17,8 @@ def test_header_declares_the_abi():
                                          'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_gae',
                                          'd1_obs_to_bf16', 'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd',
                                          'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
-                                         'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run'])
+                                         'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
+                                         'd1_sample_ar'])
 
 
 def test_library_exports_declared_symbols(pkg):
