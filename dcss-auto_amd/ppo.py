@@ -42,10 +42,9 @@ def ppo_loss(logits, values, actions, old_logp, adv, returns, clip=0.2, vcoef=0.
 
 class PPO:
     def __init__(self, model, lr=3e-4, eps=1e-5, clip=0.2, vcoef=0.5, ecoef=0.01, max_grad_norm=0.5,
-                 epochs=4, minibatch=8192, gamma=0.99, lam=0.95, autocast=True, graph=False):
+                 epochs=4, minibatch=8192, gamma=0.99, lam=0.95, autocast=True):
         self.model = model
-        self.opt = torch.optim.Adam(model.parameters(), lr=lr, eps=eps, fused=True, capturable=graph)
-        self.graph, self._g, self._g_buf = graph, None, None
+        self.opt = torch.optim.Adam(model.parameters(), lr=lr, eps=eps, fused=True)
         self.clip, self.vcoef, self.ecoef, self.max_grad_norm = clip, vcoef, ecoef, max_grad_norm
         self.epochs, self.minibatch, self.gamma, self.lam, self.autocast = epochs, minibatch, gamma, lam, autocast
 
@@ -65,8 +64,6 @@ class PPO:
         return loss.detach()
 
     def update(self, buf, generator=None):
-        if self.graph:
-            return self._update_graphed(buf, generator)
         adv, ret = self.advantages(buf)
         n = buf.T * buf.N
         obs = buf.obs.view(n, -1)
@@ -78,63 +75,6 @@ class PPO:
                 last = self.minibatch_step(obs.index_select(0, inds), actions[inds], logp[inds], adv[inds],
                                            ret[inds])
         return last
-
-    # -- HIP-graph path: one captured graph per buffer replays gather + forward + backward +
-    # clip + Adam for a minibatch whose indices sit in a static tensor. Whole minibatches only.
-    def _capture(self, buf):
-        n = buf.T * buf.N
-        if n % self.minibatch:
-            raise ValueError('graph mode needs T*N to be a multiple of the minibatch size')
-        dev = buf.obs.device
-        self._adv = torch.zeros(n, device=dev)
-        self._ret = torch.zeros(n, device=dev)
-        self._idx = torch.zeros(self.minibatch, dtype=torch.int64, device=dev)
-        obs, actions, logp = buf.obs.view(n, -1), buf.actions.view(n), buf.logp.view(n)
-
-        def step():
-            i = self._idx
-            return self.minibatch_step(obs.index_select(0, i), actions.index_select(0, i), logp.index_select(0, i),
-                                       self._adv.index_select(0, i), self._ret.index_select(0, i))
-
-        # warm-up iterations allocate optimizer state; restore the weights/state afterwards
-        saved_model = {k: v.detach().clone() for k, v in self.model.state_dict().items()}
-        saved_opt = {k: v.detach().clone() for k, v in self._opt_tensors()}
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                step()
-        torch.cuda.current_stream(dev).wait_stream(side)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self._g_loss = step()
-        with torch.no_grad():
-            for k, v in self.model.state_dict().items():
-                v.copy_(saved_model[k])
-            for k, v in self._opt_tensors():   # state created by the warm-up starts from zero
-                v.copy_(saved_opt[k]) if k in saved_opt else v.zero_()
-        self._g, self._g_buf = g, buf
-
-    def _opt_tensors(self):
-        for gi, group in enumerate(self.opt.param_groups):
-            for pi, p in enumerate(group['params']):
-                for name, v in self.opt.state.get(p, {}).items():
-                    if torch.is_tensor(v):
-                        yield (gi, pi, name), v
-
-    def _update_graphed(self, buf, generator=None):
-        if self._g is None or self._g_buf is not buf:
-            self._capture(buf)
-        adv, ret = self.advantages(buf)
-        self._adv.copy_(adv)
-        self._ret.copy_(ret)
-        n = buf.T * buf.N
-        for _ in range(self.epochs):
-            perm = torch.randperm(n, device=buf.obs.device, generator=generator)
-            for inds in perm.split(self.minibatch):
-                self._idx.copy_(inds)
-                self._g.replay()
-        return self._g_loss.detach().clone()
 
 
 # ----------------------------------------------------------------------------------------
