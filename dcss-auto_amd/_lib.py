@@ -12,7 +12,11 @@ SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd
            'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16',
            'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd', 'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
            'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
-           'd1_sample_ar')
+           'd1_sample_ar', 'd1_los_table')
+LEARN_SYMBOLS = ('learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size',
+                 'learn_action_size', 'learn_out_size', 'learn_config_bytes', 'learn_init', 'learn_step',
+                 'learn_step_active', 'learn_heuristic')
+_LEARN = {}
 
 
 def load():
@@ -43,8 +47,34 @@ def load():
         L.d1_adam_clip.argtypes = [p, p, p, p, p, C.c_int64, p, i, C.c_float, C.c_float, C.c_float, C.c_float,
                                    C.c_float, p, p]
         L.d1_gae.argtypes = [p, p, p, p, i, i, C.c_float, C.c_float, p, p, p]
+        L.d1_los_table.argtypes = [p, i, p, p, p]
         _LIB = L
     return _LIB
+
+
+def load_learn(clump=0):
+    """libd1learn_clump{0,1}.so: the learning task's learn_* ABI (include/d1learn.h)."""
+    if clump not in (0, 1):
+        raise ValueError('clump mode is 0 or 1')
+    if clump not in _LEARN:
+        path = HERE / f'libd1learn_clump{clump}.so'
+        if not path.exists():
+            raise RuntimeError(f'{path} is missing: build it with __graft_entry__.build() '
+                               '(the learning task has no CPU fallback)')
+        L = C.CDLL(str(path))
+        p, i = C.c_void_p, C.c_int
+        for name in ('learn_turn_cost', 'learn_return_gamma'):
+            getattr(L, name).restype = C.c_float
+            getattr(L, name).argtypes = []
+        for name in ('learn_state_bytes', 'learn_obs_size', 'learn_action_size', 'learn_out_size',
+                     'learn_config_bytes'):
+            getattr(L, name).argtypes = []
+        L.learn_init.argtypes = [p, i, p, p, C.c_uint64, p, p, p, i]
+        L.learn_step.argtypes = [p, i, p, p, p, i, p, p, p, p, i]
+        L.learn_step_active.argtypes = [p, i, p, p, p, i, p, p, p, p, p, i]
+        L.learn_heuristic.argtypes = [p, i, p, p, p, p, i]
+        _LEARN[clump] = L
+    return _LEARN[clump]
 
 
 def check(code, what):

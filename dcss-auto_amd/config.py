@@ -46,6 +46,37 @@ class D1WaitMap(C.Structure):
     _fields_ = [('floor', C.c_void_p), ('dist', C.c_void_p), ('starts', C.c_void_p), ('player', C.c_int32)]
 
 
+class D1LKind(C.Structure):
+    _fields_ = [('speed', C.c_int32), ('damage', C.c_int32), ('tohit', C.c_int32), ('bypass', C.c_int32)]
+
+
+class D1LConfig(C.Structure):
+    """sim::Config (gpu-d1/src/sim.h:64-67), the learning task's config (include/d1learn.h)."""
+    _fields_ = ([(k, C.c_int32) for k in ('count', 'player', 'hp', 'ac100', 'ev100', 'sh100', 'shield_limit',
+                                           'regen', 'repair')] +
+                [('gdr', C.c_int32 * 2), ('kinds', D1LKind * 6)])
+
+
+class D1LTables(C.Structure):
+    """learn::Tables with MULTI_MAP (learn_env_ring_multi.py:11-17 ctypes layout)."""
+    _fields_ = [('floor', C.c_void_p), ('cells', C.c_void_p), ('index', C.c_void_p), ('distance', C.c_void_p),
+                ('ncells', C.c_int32), ('map_ncells', C.c_void_p), ('distance_offsets', C.c_void_p),
+                ('n_maps', C.c_int32), ('map_filter', C.c_int32), ('los', C.c_void_p)]
+
+
+def learn_config(enemies=24):
+    """The reference wrapper's packing [enemies, *header[:7], 1, *gdr, *kinds]
+    (gpu-d1/branches/d1-stairs-v2/scripts/learn_env_ring_multi.py:93-97) from map 1057's
+    fixture header and roster."""
+    m = data.map1057()
+    header, kinds = m['header'], m['kinds']
+    values = [enemies, *(int(v) for v in header[:7]), 1, *gdr_table(int(header[2])),
+              *(int(v) for v in kinds.reshape(-1))]
+    c = D1LConfig()
+    C.memmove(C.addressof(c), (C.c_int32 * 35)(*values), 140)
+    return c
+
+
 RNG_PCG, RNG_COUNTER = 0, 1
 LEVEL_SHARED, LEVEL_GENERATED = 0, 1
 

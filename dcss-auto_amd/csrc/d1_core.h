@@ -1,0 +1,559 @@
+// d1hip core: device code shared by the environment, wait and learning-task kernels.
+//
+// Wave-uniform RNG (PCG32 / Philox counter mode), 80x70 LDS bitmaps (70 rows x 3
+// dwords), the player view, the bit-parallel distance field, melee and monster
+// pathing of gpu-d1/src/sim.h. Everything is force-inlined into the kernels that
+// include it; nothing here allocates or keeps state.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/d1hip.h"
+
+namespace d1 {
+
+constexpr int W = 80, H = 70, N = 5600, RW = 3;   // 3 dwords per 80-bit row
+constexpr int ROWS_WORDS = H * RW;                // 210
+constexpr int BIG = 1 << 20;
+
+struct Smem {
+    uint32_t floor[ROWS_WORDS];
+    uint32_t viewed[ROWS_WORDS];
+    uint32_t occ[ROWS_WORDS];
+    uint32_t reach[ROWS_WORDS];
+    uint32_t front[ROWS_WORDS];
+    union {
+        uint8_t dist[N];        // BFS layer mod 256, valid where `reach` is set (monster phase)
+        struct {
+            uint32_t win[225];  // observation window: kind+1 | hp<<8 | stair<<16 (observation)
+            int32_t rowpre[72]; // inclusive per-row prefix counts (episode reset)
+        };
+    };
+};
+
+// ---------------------------------------------------------------- small helpers
+__device__ __forceinline__ int lane_id() { return (int)threadIdx.x; }
+__device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+__device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
+__device__ __forceinline__ int iabs(int a) { return a < 0 ? -a : a; }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int lane_val(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
+__device__ __forceinline__ int wave_max(int v) {
+    for (int o = 32; o; o >>= 1) v = imax(v, __shfl_xor(v, o));
+    return uni(v);
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+    for (int o = 32; o; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
+    return (uint32_t)uni((int)v);
+}
+// gpu-d1/src/sim.h:14
+__device__ __forceinline__ int cheb(int a, int b) { return imax(iabs(a % W - b % W), iabs(a / W - b / W)); }
+// gpu-d1/src/sim.h:201-206: N, E, S, W, NE, SE, SW, NW
+__device__ __forceinline__ int nbr(int p, int d) {
+    int ddx = d == 1 || d == 4 || d == 5 ? 1 : d == 3 || d == 6 || d == 7 ? -1 : 0;
+    int ddy = d == 0 || d == 4 || d == 7 ? -1 : d == 2 || d == 5 || d == 6 ? 1 : 0;
+    int x = p % W + ddx, y = p / W + ddy;
+    return x >= 0 && x < W && y >= 0 && y < H ? y * W + x : -1;
+}
+__device__ __forceinline__ bool inb(int x, int y) { return x >= 0 && x < W && y >= 0 && y < H; }
+__device__ __forceinline__ bool bit_at(const uint32_t *bm, int x, int y) {
+    return (bm[y * RW + (x >> 5)] >> (x & 31)) & 1u;
+}
+__device__ __forceinline__ bool bit(const uint32_t *bm, int p) { return bit_at(bm, p % W, p / W); }
+
+struct Row {
+    uint32_t a, b, c;   // bits 0-31, 32-63, 64-79
+};
+__device__ __forceinline__ Row row_ld(const uint32_t *bm, int y) { return {bm[y * RW], bm[y * RW + 1], bm[y * RW + 2]}; }
+__device__ __forceinline__ void row_st(uint32_t *bm, int y, Row r) { bm[y * RW] = r.a; bm[y * RW + 1] = r.b; bm[y * RW + 2] = r.c; }
+__device__ __forceinline__ Row row_or(Row x, Row y) { return {x.a | y.a, x.b | y.b, x.c | y.c}; }
+__device__ __forceinline__ Row row_and(Row x, Row y) { return {x.a & y.a, x.b & y.b, x.c & y.c}; }
+__device__ __forceinline__ Row row_andn(Row x, Row y) { return {x.a & ~y.a, x.b & ~y.b, x.c & ~y.c}; }
+__device__ __forceinline__ Row row_shl1(Row r) { return {r.a << 1, (r.b << 1) | (r.a >> 31), ((r.c << 1) | (r.b >> 31)) & 0xFFFFu}; }
+__device__ __forceinline__ Row row_shr1(Row r) { return {(r.a >> 1) | (r.b << 31), (r.b >> 1) | (r.c << 31), r.c >> 1}; }
+__device__ __forceinline__ bool row_any(Row r) { return (r.a | r.b | r.c) != 0; }
+__device__ __forceinline__ int row_popc(Row r) { return __popc(r.a) + __popc(r.b) + __popc(r.c); }
+// bits [x0, x1] of the 32-bit word starting at bit `base`
+__device__ __forceinline__ uint32_t word_range(int x0, int x1, int base) {
+    int lo = imax(x0 - base, 0), hi = imin(x1 - base, 31);
+    return lo > hi ? 0u : ((hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u)) & ~((1u << lo) - 1u));
+}
+// bits [x0, x1] (inclusive, clipped to 0..79)
+__device__ __forceinline__ Row row_range(int x0, int x1) {
+    x0 = imax(x0, 0);
+    x1 = imin(x1, W - 1);
+    if (x0 > x1) return Row{0, 0, 0};
+    return Row{word_range(x0, x1, 0), word_range(x0, x1, 32), word_range(x0, x1, 64) & 0xFFFFu};
+}
+// 15-bit window pattern v (bit k = x px-7+k) placed on an 80-bit row
+__device__ __forceinline__ Row row_place15(uint32_t v, int px) {
+    int shift = px - 7;
+    uint64_t lo, hi;
+    if (shift < 0) { lo = (uint64_t)v >> (-shift); hi = 0; }
+    else if (shift < 64) { lo = (uint64_t)v << shift; hi = shift ? ((uint64_t)v >> (64 - shift)) : 0; }
+    else { lo = 0; hi = (uint64_t)v << (shift - 64); }
+    return {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi & 0xFFFFu};
+}
+// position of the j-th set bit (j < popc(v))
+__device__ __forceinline__ int select32(uint32_t v, int j) {
+    int pos = 0;
+    for (int s = 16; s; s >>= 1) {
+        int c = __popc(v & ((1u << s) - 1u));
+        if (j >= c) { j -= c; v >>= s; pos += s; }
+    }
+    return pos;
+}
+__device__ __forceinline__ int row_select(Row r, int j) {
+    int c0 = __popc(r.a);
+    if (j < c0) return select32(r.a, j);
+    j -= c0;
+    int c1 = __popc(r.b);
+    if (j < c1) return 32 + select32(r.b, j);
+    return 64 + select32(r.c, j - c1);
+}
+__device__ __forceinline__ uint32_t fmix32(uint32_t h) {
+    h ^= h >> 16; h *= 0x85ebca6bu; h ^= h >> 13; h *= 0xc2b2ae35u; h ^= h >> 16;
+    return h;
+}
+__device__ __forceinline__ uint32_t term(uint32_t word, uint32_t index) { return fmix32(word ^ (index * 0x9E3779B9u)); }
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {   // gpu-d1/src/sim.h:15-20
+    x += 0x9e3779b97f4a7c15ULL;
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebULL;
+    return x ^ (x >> 31);
+}
+
+// ---------------------------------------------------------------- RNG (wave-uniform)
+// PCG32 XSH-RR as gpu-d1/src/sim.h:21-60, or Philox4x32-10 where draw k of stream
+// (t, env, domain) is word k%4 of Philox(ctr={k/4, t, env, domain}, key=seed).
+struct Rng {
+    uint64_t st, inc;
+    uint32_t key0, key1, t, env, dom, k;
+    uint32_t blk;
+    unsigned __int128 buf;   // the current Philox block, word j at bits 32j (no indexed fields)
+    int mode;
+
+    __device__ __forceinline__ void philox_block(uint32_t b) {
+        uint32_t c0 = b, c1 = t, c2 = env, c3 = dom, k0 = key0, k1 = key1;
+#pragma unroll
+        for (int r = 0; r < 10; r++) {
+            uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+            uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+            uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+            c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+            k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+        }
+        buf = (unsigned __int128)c0 | ((unsigned __int128)c1 << 32) | ((unsigned __int128)c2 << 64) |
+              ((unsigned __int128)c3 << 96);
+        blk = b;
+    }
+    __device__ __forceinline__ uint32_t next() {
+        if (mode == 0) {
+            uint64_t old = st;
+            st = old * 6364136223846793005ULL + (inc | 1);
+            uint32_t x = (uint32_t)(((old >> 18) ^ old) >> 27), r = (uint32_t)(old >> 59);
+            return (x >> r) | (x << ((0u - r) & 31u));
+        }
+        uint32_t b = k >> 2;
+        if (b != blk) philox_block(b);
+        uint32_t j = k & 3u;
+        k++;
+        return (uint32_t)(buf >> (32 * j));
+    }
+    __device__ __forceinline__ int r(int bound) {   // gpu-d1/src/sim.h:36-51
+        if (bound <= 1) return 0;
+        uint32_t x = next();
+        uint64_t m = (uint64_t)x * (uint32_t)bound;
+        uint32_t low = (uint32_t)m;
+        if (low < (uint32_t)bound) {
+            uint32_t th = (0u - (uint32_t)bound) % (uint32_t)bound;
+            while (low < th) {
+                x = next();
+                m = (uint64_t)x * (uint32_t)bound;
+                low = (uint32_t)m;
+            }
+        }
+        return (int)(m >> 32);
+    }
+    __device__ __forceinline__ int avg(int n) { int a = r(n); return (a + r(n + 1)) / 2; }             // sim.h:52-55
+    __device__ __forceinline__ int round(int n, int d) { int rem = n % d; return n / d + (rem && r(d) < rem); }  // sim.h:56-59
+    __device__ __forceinline__ void pcg_seed(uint64_t s, uint64_t seq) {   // sim.h:29-35
+        mode = 0; st = 0; inc = (seq << 1) | 1;
+        next();
+        st += s;
+        next();
+    }
+    __device__ __forceinline__ void counter(uint64_t key, uint32_t e, uint32_t tt, uint32_t d) {
+        mode = 1; key0 = (uint32_t)key; key1 = (uint32_t)(key >> 32); env = e; t = tt; dom = d; k = 0; blk = 0xFFFFFFFFu;
+        st = 0; inc = 0;
+    }
+};
+
+// PCG jump-ahead: state after j steps = A[j]*s + C[j]*inc (A[j] = a^j, C[j] = sum_{i<j} a^i).
+struct PcgJump {
+    uint64_t a[65], c[65];
+    constexpr PcgJump() : a(), c() {
+        a[0] = 1; c[0] = 0;
+        for (int j = 1; j <= 64; j++) { a[j] = a[j - 1] * 6364136223846793005ULL; c[j] = c[j - 1] * 6364136223846793005ULL + 1; }
+    }
+};
+__constant__ constexpr PcgJump kJump{};
+
+__device__ __forceinline__ uint32_t pcg_out(uint64_t old) {
+    uint32_t x = (uint32_t)(((old >> 18) ^ old) >> 27), r = (uint32_t)(old >> 59);
+    return (x >> r) | (x << ((0u - r) & 31u));
+}
+// Reservoir choice over `total` eligible cells: the 1-based count c is kept when
+// r(c) == 0, the last kept count wins (gpu-d1/branches/d1-stairs-v2/src/learn.cu:432-441).
+// 64 counts per pass: lane l evaluates count c0+l from the draw it would get if no
+// earlier draw in the pass were rejected; a pass in which any Lemire rejection is
+// possible (low < bound) is replayed serially, so the draw sequence is the serial one.
+__device__ __forceinline__ int reservoir(Rng &s, int total, int lane) {
+    int chosen = total >= 1 ? 0 : -1;
+    int c0 = 2;
+    while (c0 <= total) {
+        int cnt = imin(64, total - c0 + 1);
+        int c = c0 + lane;
+        uint32_t xw;
+        if (s.mode == 0) {
+            uint64_t old = kJump.a[lane] * s.st + kJump.c[lane] * s.inc;
+            xw = pcg_out(old);
+        } else {
+            uint32_t kk = s.k + (uint32_t)lane;
+            Rng tmp = s;
+            tmp.philox_block(kk >> 2);
+            xw = (uint32_t)(tmp.buf >> (32 * (kk & 3u)));
+        }
+        uint64_t m = (uint64_t)xw * (uint32_t)c;
+        bool act = lane < cnt;
+        bool risky = act && (uint32_t)m < (uint32_t)c;
+        if (ballot(risky)) {
+            for (int cc = c0; cc < c0 + cnt; cc++) if (s.r(cc) == 0) chosen = cc - 1;
+        } else {
+            uint64_t keep = ballot(act && (m >> 32) == 0);
+            if (keep) chosen = c0 + 63 - __clzll((long long)keep) - 1;
+            if (s.mode == 0) s.st = kJump.a[cnt] * s.st + kJump.c[cnt] * s.inc;
+            else s.k += (uint32_t)cnt;
+        }
+        c0 += cnt;
+    }
+    return chosen;
+}
+
+// ---------------------------------------------------------------- world context
+struct Ctx {
+    Smem *sm;
+    const D1Config *c;
+    const uint64_t *rays;   // [nslots][64]
+    int nslots;
+    Rng g;
+    int player, hp, regen, blocks, ticks, killed, decisions, floor_seen, episode, first_stair_tick, ncells;
+    uint64_t stairs;   // three int16 cells at bits 0, 16, 32 (-1 = none)
+    uint32_t t, env_id;
+    uint64_t vis0, vis1, vis2, vis3;   // player view, quadrants (+,+) (-,+) (-,-) (+,-)
+    bool adj_clear;                     // the 8 neighbours of any cell are always in view
+    // this lane's monster (lane < count)
+    int mpos, mhp, menergy, mawake, mkind;
+    int lane;
+};
+
+__device__ __forceinline__ int stair_at(const Ctx &x, int k) { return (int16_t)(uint16_t)(x.stairs >> (16 * k)); }
+__device__ __forceinline__ uint64_t pack_stairs(int a, int b, int c) {
+    return (uint64_t)(uint16_t)a | (uint64_t)(uint16_t)b << 16 | (uint64_t)(uint16_t)c << 32;
+}
+__device__ __forceinline__ bool seen_at(const Ctx &x, int p) { return bit(x.sm->viewed, p) && bit(x.sm->floor, p); }
+
+// 15x15 view lookup of the cell (dx, dy) from the player
+__device__ __forceinline__ bool vis_rel(const Ctx &x, int dx, int dy) {
+    if (iabs(dx) > 7 || iabs(dy) > 7) return false;
+    int b = iabs(dy) * 8 + iabs(dx);
+    uint64_t v = 0;
+    if (dx >= 0 && dy >= 0) v |= x.vis0;
+    if (dx <= 0 && dy >= 0) v |= x.vis1;
+    if (dx <= 0 && dy <= 0) v |= x.vis2;
+    if (dx >= 0 && dy <= 0) v |= x.vis3;
+    return (v >> b) & 1;
+}
+// in_view, gpu-d1/branches/d1-stairs-v2/src/learn.cu:192-198 (terrain LOS, radius 7)
+__device__ __forceinline__ bool in_view(const Ctx &x, int p) {
+    if (p < 0) return false;
+    return vis_rel(x, p % W - x.player % W, p / W - x.player / W);
+}
+__device__ __forceinline__ bool q_sx(int q) { return q == 0 || q == 3; }   // +x quadrants
+__device__ __forceinline__ bool q_sy(int q) { return q < 2; }              // +y quadrants
+
+// Opaque inside-blocker set of quadrant q around (ox, oy): lane j tests blocker
+// (j%8, j/8) (gpu-d1/scripts/compile_fixture.py:35-39; out-of-bounds cells are clear).
+__device__ __forceinline__ uint64_t opaque_set(const Ctx &x, int ox, int oy, int q) {
+    int cx = ox + (q_sx(q) ? 1 : -1) * (x.lane & 7), cy = oy + (q_sy(q) ? 1 : -1) * (x.lane >> 3);
+    bool op = inb(cx, cy) && !bit_at(x.sm->floor, cx, cy);
+    return ballot(op);
+}
+// Player field of view: vis_q bit j set when target (j%8, j/8) of quadrant q is in
+// bounds and one of its rays misses every opaque blocker.
+__device__ __forceinline__ void compute_view(Ctx &x) {
+    int px = x.player % W, py = x.player / W;
+    uint64_t o0 = opaque_set(x, px, py, 0), o1 = opaque_set(x, px, py, 1);
+    uint64_t o2 = opaque_set(x, px, py, 2), o3 = opaque_set(x, px, py, 3);
+    bool a0 = false, a1 = false, a2 = false, a3 = false;
+    for (int s = 0; s < x.nslots; s++) {
+        uint64_t m = x.rays[s * 64 + x.lane];
+        a0 |= (m & o0) == 0; a1 |= (m & o1) == 0; a2 |= (m & o2) == 0; a3 |= (m & o3) == 0;
+    }
+    int tx = x.lane & 7, ty = x.lane >> 3;
+    x.vis0 = ballot(a0 && inb(px + tx, py + ty));
+    x.vis1 = ballot(a1 && inb(px - tx, py + ty));
+    x.vis2 = ballot(a2 && inb(px - tx, py - ty));
+    x.vis3 = ballot(a3 && inb(px + tx, py - ty));
+}
+// LOS from a monster to the player within Chebyshev 6 (monster_detects_player,
+// gpu-d1/branches/d1-stairs-v2/src/learn.cu:199-207).
+__device__ __forceinline__ bool detects(Ctx &x, int origin) {
+    int ox = origin % W, oy = origin / W, dx = x.player % W - ox, dy = x.player / W - oy;
+    if (iabs(dx) > 6 || iabs(dy) > 6) return false;
+    if (!x.c->wake_los) return true;
+    int t = iabs(dy) * 8 + iabs(dx);
+    bool det = false;
+    for (int q = 0; q < 4; q++) {
+        bool sx = q_sx(q), sy = q_sy(q);
+        if ((dx && (dx > 0) != sx) || (dy && (dy > 0) != sy)) continue;
+        uint64_t opq = opaque_set(x, ox, oy, q);
+        bool alive = x.lane < x.nslots && (x.rays[imin(x.lane, x.nslots - 1) * 64 + t] & opq) == 0;
+        det |= ballot(alive) != 0;
+    }
+    return det;
+}
+
+// Reveal, gpu-d1/branches/d1-stairs-v2/src/learn.cu:298-333: viewed |= view; returns
+// the number of floor cells seen for the first time (seen == viewed floor).
+__device__ __forceinline__ int reveal(Ctx &x) {
+    compute_view(x);
+    int px = x.player % W, py = x.player / W;
+    int fresh = 0;
+    int dy = x.lane - 7, y = py + dy;
+    bool mine = x.lane < 15 && y >= 0 && y < H;
+    Row mask{0, 0, 0};
+    if (mine) {
+        int ay = iabs(dy);
+        uint32_t R = 0, L = 0;
+        if (dy >= 0) { R |= (uint32_t)(x.vis0 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis1 >> (8 * ay)) & 0xFFu; }
+        if (dy <= 0) { R |= (uint32_t)(x.vis3 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis2 >> (8 * ay)) & 0xFFu; }
+        uint32_t v15 = (__builtin_bitreverse32(L) >> 24) | (R << 7);
+        mask = row_place15(v15, px);
+        Row old = row_ld(x.sm->viewed, y);
+        Row fl = row_ld(x.sm->floor, y);
+        fresh = row_popc(row_and(row_andn(mask, old), fl));
+    }
+    __syncthreads();
+    if (mine) row_st(x.sm->viewed, y, row_or(mask, row_ld(x.sm->viewed, y)));
+    __syncthreads();
+    int total = (int)wave_sum((uint32_t)fresh);
+    x.floor_seen += total;
+    return total;
+}
+
+__device__ __forceinline__ int stair_index(const Ctx &x) {
+    for (int k = 0; k < 3; k++) if (stair_at(x, k) >= 0 && x.player == stair_at(x, k)) return k + 1;
+    return 0;
+}
+__device__ __forceinline__ int known_stairs(const Ctx &x) {
+    int n = 0;
+    for (int k = 0; k < 3; k++) n += stair_at(x, k) >= 0 && seen_at(x, stair_at(x, k));
+    return n;
+}
+__device__ __forceinline__ bool visible_awake(const Ctx &x) {
+    bool me = x.lane < x.c->count && x.mhp > 0 && x.mawake && in_view(x, x.mpos);
+    return ballot(me) != 0;
+}
+__device__ __forceinline__ void occ_set(Ctx &x, int p, bool on) {
+    if (x.lane == 0) {
+        uint32_t *w = &x.sm->occ[(p / W) * RW + ((p % W) >> 5)];
+        uint32_t b = 1u << ((p % W) & 31);
+        *w = on ? (*w | b) : (*w & ~b);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void occ_set_lane(Ctx &x, int p) {
+    atomicOr(&x.sm->occ[(p / W) * RW + ((p % W) >> 5)], 1u << ((p % W) & 31));
+}
+__device__ __forceinline__ void occ_clear_lane(Ctx &x, int p) {
+    atomicAnd(&x.sm->occ[(p / W) * RW + ((p % W) >> 5)], ~(1u << ((p % W) & 31)));
+}
+
+// ---------------------------------------------------------------- cell selection
+// Row prefix counts of a bitmap (rows in `bm`), stored inclusive in sm->rowpre.
+__device__ __forceinline__ int row_prefix(Ctx &x, const uint32_t *bm) {
+    int y0 = x.lane, y1 = x.lane + 64;
+    int c0 = row_popc(row_ld(bm, y0));
+    int c1 = y1 < H ? row_popc(row_ld(bm, y1)) : 0;
+    int s0 = c0;
+    for (int o = 1; o < 64; o <<= 1) { int v = __shfl_up(s0, o); if (x.lane >= o) s0 += v; }
+    int tot0 = lane_val(s0, 63);
+    int s1 = c1;
+    for (int o = 1; o < 64; o <<= 1) { int v = __shfl_up(s1, o); if (x.lane >= o) s1 += v; }
+    __syncthreads();
+    x.sm->rowpre[y0] = s0;
+    if (y1 < H) x.sm->rowpre[y1] = s1 + tot0;
+    __syncthreads();
+    return x.sm->rowpre[H - 1];
+}
+// The k-th set cell (row-major) of bitmap `bm`, given its rowpre.
+__device__ __forceinline__ int select_cell(Ctx &x, const uint32_t *bm, int k) {
+    int lo = 0, hi = H - 1;   // first row with rowpre > k
+    while (lo < hi) { int mid = (lo + hi) >> 1; if (x.sm->rowpre[mid] > k) hi = mid; else lo = mid + 1; }
+    int before = lo ? x.sm->rowpre[lo - 1] : 0;
+    return lo * W + row_select(row_ld(bm, lo), k - before);
+}
+
+// ---------------------------------------------------------------- monsters
+__device__ __forceinline__ int kind_speed(const D1Config *c, int k) {
+    int s = c->kinds[0].speed;
+    s = k == 1 ? c->kinds[1].speed : s;
+    s = k == 2 ? c->kinds[2].speed : s;
+    s = k == 3 ? c->kinds[3].speed : s;
+    s = k == 4 ? c->kinds[4].speed : s;
+    s = k == 5 ? c->kinds[5].speed : s;
+    return s;
+}
+// gpu-d1/src/sim.h:130-163 (kind = the acting monster's kind)
+__device__ __forceinline__ void attack(Ctx &x, int kind) {
+    const D1Config *c = x.c;
+    const D1Kind &k = c->kinds[kind];
+    Rng &r = x.g;
+    int hit = r.r(k.tohit + 1);
+    int ev = r.round(c->ev100, 100);
+    ev = r.avg(2 * ev);
+    int margin = hit - ev;
+    if (r.r(100) < 5) margin = (r.r(2) ? 1 : -1) * 1000;
+    int bypass = r.r(k.bypass);
+    int sh = r.round(c->sh100, 100);
+    int block = r.avg(sh * 2) / 3 - 1;
+    if (block >= bypass && x.blocks < c->shield_limit) { x.blocks++; return; }
+    if (margin < 0) return;
+    int damage = 1 + r.r(k.damage);
+    int ac = r.round(c->ac100, 100);
+    int gac = r.round(c->ac100, 100);
+    int gdr = c->gdr[imin(imax(gac - c->ac100 / 100, 0), 1)];
+    int saved = r.r(ac + 1);
+    int half = r.round(ac, 2);
+    saved = imax(saved, imin(gdr * k.damage / 100, half));
+    damage = imax(0, damage - saved);
+    x.hp -= damage;
+}
+// distance of q relative to p (both via the BFS field); BIG when q was not reached
+__device__ __forceinline__ int rel_dist(const Ctx &x, int q, int p) {
+    if (!bit(x.sm->reach, q)) return BIG;
+    return (int)(int8_t)(uint8_t)(x.sm->dist[q] - x.sm->dist[p]);
+}
+__device__ __forceinline__ bool walkable(const Ctx &x, int q) {
+    return q >= 0 && bit(x.sm->floor, q) && q != x.player && !bit(x.sm->occ, q);
+}
+// gpu-d1/src/sim.h:207-253: greedy descent with rotated order and 1/ties
+// replacement, then a bounded 24-node BFS detour when stuck.
+__device__ __forceinline__ int choose_move(Ctx &x, int p) {
+    int rotation = x.g.r(4);
+    int z = x.lane & 7;
+    int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
+    int q = nbr(p, d);
+    bool ok = x.lane < 8 && walkable(x, q);
+    int rel = ok ? rel_dist(x, q, p) : BIG;
+    uint64_t okm = ballot(ok);
+    int best = -1, bd = 0, ties = 0;
+    for (int zz = 0; zz < 8; zz++) {
+        if (!((okm >> zz) & 1)) continue;
+        int dd = lane_val(rel, zz), qq = lane_val(q, zz);
+        if (dd < bd) { bd = dd; best = qq; ties = 1; }
+        else if (dd == bd && best >= 0 && x.g.r(++ties) == 0) best = qq;
+    }
+    if (best >= 0 || !x.c->repair) return best;
+    // queue: lane j holds cells[j] and first[j]
+    int qcell = x.lane == 0 ? p : -1, qfirst = -1, len = 1;
+    for (int head = 0; head < len; head++) {
+        int cell = lane_val(qcell, head);
+        int hfirst = lane_val(qfirst, head);
+        int nq = nbr(cell, x.lane & 7);
+        bool v = x.lane < 8 && walkable(x, nq);
+        uint64_t vm = ballot(v);
+        for (int dd = 0; dd < 8; dd++) {
+            if (!((vm >> dd) & 1)) continue;
+            int qq = lane_val(nq, dd);
+            if (ballot(x.lane < len && qcell == qq)) continue;
+            int step = head == 0 ? qq : hfirst;
+            if (rel_dist(x, qq, p) < 0) return step;
+            if (len < 24) {
+                if (x.lane == len) { qcell = qq; qfirst = step; }
+                len++;
+            }
+        }
+    }
+    return -1;
+}
+// One BFS layer for row y: dilate the frontier rows y-1..y+1 by one cell, keep floor
+// cells not reached yet.
+__device__ __forceinline__ Row bfs_expand(const Smem *sm, int y) {
+    Row v = row_ld(sm->front, y);
+    if (y > 0) v = row_or(v, row_ld(sm->front, y - 1));
+    if (y < H - 1) v = row_or(v, row_ld(sm->front, y + 1));
+    v = row_or(v, row_or(row_shl1(v), row_shr1(v)));
+    return row_andn(row_and(v, row_ld(sm->floor, y)), row_ld(sm->reach, y));
+}
+__device__ __forceinline__ void scatter_layer(Smem *sm, int base, uint32_t b, int layer) {
+    while (b) {
+        int xx = __ffs(b) - 1;
+        b &= b - 1;
+        sm->dist[base + xx] = (uint8_t)layer;
+    }
+}
+__device__ __forceinline__ void bfs_commit(Smem *sm, int y, Row nw, int layer) {
+    row_st(sm->front, y, nw);
+    row_st(sm->reach, y, row_or(row_ld(sm->reach, y), nw));
+    scatter_layer(sm, y * W, nw.a, layer);
+    scatter_layer(sm, y * W + 32, nw.b, layer);
+    scatter_layer(sm, y * W + 64, nw.c, layer);
+}
+// Bit-parallel BFS over floor from the player (the all-pairs row of
+// gpu-d1/scripts/learn_env.py:31-39), stopped `margin` layers after every mover is
+// reached. dist holds the layer mod 256; comparisons are relative (|delta| <= 25).
+__device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
+    Smem *sm = x.sm;
+    for (int w = x.lane; w < ROWS_WORDS; w += 64) { sm->reach[w] = 0; sm->front[w] = 0; }
+    __syncthreads();
+    if (x.lane == 0) {
+        int p = x.player;
+        sm->reach[(p / W) * RW + ((p % W) >> 5)] |= 1u << ((p % W) & 31);
+        sm->front[(p / W) * RW + ((p % W) >> 5)] |= 1u << ((p % W) & 31);
+        sm->dist[p] = 0;
+    }
+    __syncthreads();
+    int stop = 1 << 30;
+    const int y0 = x.lane, y1 = x.lane + 64;
+    for (int layer = 1; layer < N; layer++) {
+        Row n0 = bfs_expand(sm, y0), n1 = y1 < H ? bfs_expand(sm, y1) : Row{0, 0, 0};
+        __syncthreads();
+        bfs_commit(sm, y0, n0, layer);
+        if (y1 < H) bfs_commit(sm, y1, n1, layer);
+        __syncthreads();
+        if (!ballot(row_any(n0) || row_any(n1))) break;
+        if (stop == (1 << 30)) {
+            bool missing = ((movers >> x.lane) & 1) && !bit(sm->reach, x.mpos);
+            if (!ballot(missing)) stop = layer + margin;
+        }
+        if (layer >= stop) break;
+    }
+}
+// gpu-d1/src/sim.h:254-269
+__device__ __forceinline__ void act(Ctx &x, int id) {
+    if (x.lane == id) x.menergy -= 10;
+    int p = lane_val(x.mpos, id);
+    if (cheb(p, x.player) == 1) { attack(x, lane_val(x.mkind, id)); return; }
+    int q = choose_move(x, p);
+    if (q >= 0) {
+        occ_set(x, p, false);
+        occ_set(x, q, true);
+        if (x.lane == id) x.mpos = q;
+    }
+}
+
+}  // namespace d1

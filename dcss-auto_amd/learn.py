@@ -1,0 +1,144 @@
+"""The reference's d1-stairs-v2 learning task on the HIP `learn_*` library.
+
+`LearnEnv` keeps the constructor, buffers and `reset / step / heuristic` of
+gpu-d1/branches/d1-stairs-v2/scripts/learn_env_ring_multi.py:61-120, so a trainer
+written against that wrapper runs unchanged: obs float [B, 1015], mask float [B, 19],
+out float [B, 45], int64 actions, optional bool `active`. `LearnMaps` builds the
+library's map tables on the device from byte floor maps: cells (all floor cells in
+row-major order, the corpus compiler's rule, gpu-d1/scripts/compile_corpus.py:37-40),
+and the LOS table by the HIP LOS compiler (`d1_los_table`). There is no host path:
+the library refuses `gpu=0` and this module needs a GPU device.
+"""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _lib, data
+from .config import D1LTables, D1Tables, learn_config
+
+N = 5600
+
+
+class LearnMaps:
+    """Device map tables for one or more 80x70 byte floor maps (nonzero = floor)."""
+
+    def __init__(self, floors=None, device='cuda'):
+        if floors is None:
+            floors = data.map1057()['floor'][None]
+        floors = np.ascontiguousarray(np.asarray(floors, np.uint8).reshape(-1, N))
+        self.n_maps = len(floors)
+        cells = np.full((self.n_maps, N), -1, np.int16)
+        ncells = np.zeros(self.n_maps, np.int32)
+        for m, f in enumerate(floors):
+            c = np.flatnonzero(f).astype(np.int16)
+            cells[m, :len(c)] = c
+            ncells[m] = len(c)
+        self.device = torch.device(device)
+        self.floor = torch.from_numpy(floors).to(self.device)
+        self.cells = torch.from_numpy(cells).to(self.device)
+        self.ncells = torch.from_numpy(ncells).to(self.device)
+        self.cell_counts = ncells
+        self.los = torch.empty((self.n_maps, N, 10), dtype=torch.int32, device=self.device)
+        slots = np.ascontiguousarray(data.rays()['slots'], np.uint64)
+        self._slots = torch.from_numpy(slots.view(np.int64)).to(self.device)
+        rays = D1Tables(None, None, self._slots.data_ptr(), slots.shape[0])
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.check(_lib.load().d1_los_table(self.floor.data_ptr(), self.n_maps, C.byref(rays), self.los.data_ptr(),
+                                            stream), 'd1_los_table')
+
+    def tables(self, map_filter=-1):
+        """The library's Tables struct; index/distance are not read by this library."""
+        if not -2 <= map_filter < self.n_maps:
+            raise ValueError('map_filter is -2 (balanced first episodes), -1 (random) or a map index')
+        return D1LTables(self.floor.data_ptr(), self.cells.data_ptr(), None, None, int(self.cell_counts[0]),
+                         self.ncells.data_ptr(), None, self.n_maps, map_filter, self.los.data_ptr())
+
+
+class LearnEnv:
+    def __init__(self, batch=512, enemies=24, seed=0, device='cuda', limit=2048, maps=None, map_filter=-1,
+                 clump=0):
+        if enemies != 24 or limit < 1:
+            raise ValueError('the d1-stairs-v2 task places exactly 24 enemies')
+        self.device = torch.device('cuda:0' if device == 'cuda' else device)
+        if self.device.type != 'cuda':
+            raise RuntimeError('the learning task runs on the GPU only (no host path)')
+        self.batch, self.enemies, self.limit = batch, enemies, limit
+        self.lib = _lib.load_learn(clump)
+        self.maps = maps if maps is not None else LearnMaps(device=self.device)
+        self.tables = self.maps.tables(map_filter)
+        self.config = learn_config(enemies)
+        assert C.sizeof(self.config) == self.lib.learn_config_bytes()
+        self.state = torch.zeros((batch, self.lib.learn_state_bytes()), dtype=torch.uint8, device=self.device)
+        self.obs = torch.empty((batch, self.lib.learn_obs_size()), device=self.device)
+        self.action_size = self.lib.learn_action_size()
+        self.out_size = self.lib.learn_out_size()
+        self.mask = torch.empty((batch, self.action_size), device=self.device)
+        self.out = torch.zeros((batch, self.out_size), device=self.device)
+        self.actions = torch.empty(batch, dtype=torch.int64, device=self.device)
+        self.reset(seed)
+
+    @property
+    def stream(self):
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def check(self, code):
+        if code:
+            raise RuntimeError(f'learning task call failed with error {code}')
+
+    def reset(self, seed):
+        self.check(self.lib.learn_init(self.state.data_ptr(), self.batch, C.byref(self.config),
+                                       C.byref(self.tables), seed, self.obs.data_ptr(), self.mask.data_ptr(),
+                                       self.stream, 1))
+        return self.obs
+
+    def step(self, actions, active=None):
+        assert actions.device == self.device and actions.dtype == torch.int64 and actions.is_contiguous()
+        if active is not None:
+            assert active.device == self.device and active.dtype == torch.bool and active.is_contiguous()
+            assert active.shape == (self.batch,)
+            self.check(self.lib.learn_step_active(self.state.data_ptr(), self.batch, C.byref(self.config),
+                                                  C.byref(self.tables), actions.data_ptr(), self.limit,
+                                                  self.obs.data_ptr(), self.mask.data_ptr(), self.out.data_ptr(),
+                                                  active.data_ptr(), self.stream, 1))
+            return self.obs, self.out
+        self.check(self.lib.learn_step(self.state.data_ptr(), self.batch, C.byref(self.config),
+                                       C.byref(self.tables), actions.data_ptr(), self.limit, self.obs.data_ptr(),
+                                       self.mask.data_ptr(), self.out.data_ptr(), self.stream, 1))
+        return self.obs, self.out
+
+    def heuristic(self):
+        self.check(self.lib.learn_heuristic(self.state.data_ptr(), self.batch, C.byref(self.config),
+                                            C.byref(self.tables), self.actions.data_ptr(), self.stream, 1))
+        return self.actions
+
+    def errors(self):
+        """Envs whose last reset found no clump anchor or stair cell (the reference asserts)."""
+        return self.state[:, ROW_DTYPE.fields['error'][1]].nonzero().flatten()
+
+
+# Row layout (d1_learn.hip): header, 24 enemies, viewed and floor bitmaps, frontier list.
+ROW_DTYPE = np.dtype([
+    ('rng_state', '<u8'), ('rng_inc', '<u8'), ('encountered', '<u8'),
+    ('ticks', '<i4'), ('killed', '<i4'), ('decisions', '<i4'), ('floor_seen', '<i4'), ('episode', '<i4'),
+    ('first_stair_tick', '<i4'), ('player', '<i2'), ('hp', '<i2'), ('regen', '<i2'), ('blocks', '<i2'),
+    ('map_id', '<i2'), ('next_slot', '<i2'), ('frontier_count', '<i2'), ('stairs', '<i2', 3),
+    ('clumped', 'u1'), ('error', 'u1'), ('pad', 'u1', 10),
+    ('mon', [('pos', '<i2'), ('hp', '<i2'), ('energy', '<i2'), ('awake', 'u1'), ('slot', 'i1')], 24),
+    ('viewed', '<u4', 210), ('floor', '<u4', 210), ('frontier', '<u2', N)])
+
+
+def decode_rows(state):
+    """Structured view of learn state rows (a [B, learn_state_bytes] uint8 array)."""
+    a = np.ascontiguousarray(np.asarray(state, np.uint8))
+    return np.frombuffer(a.tobytes(), dtype=np.dtype({'names': ROW_DTYPE.names,
+                                                      'formats': [ROW_DTYPE.fields[n][0] for n in ROW_DTYPE.names],
+                                                      'offsets': [ROW_DTYPE.fields[n][1] for n in ROW_DTYPE.names],
+                                                      'itemsize': a.shape[1]}))
+
+
+def bitmap_cells(words):
+    """uint32 [210] rows-of-3-dwords bitmap -> bool [5600]."""
+    w = np.asarray(words, np.uint32).reshape(70, 3)
+    bits = ((w[:, :, None] >> np.arange(32, dtype=np.uint32)) & 1).reshape(70, 96)[:, :80]
+    return bits.reshape(-1).astype(bool)

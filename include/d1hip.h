@@ -126,6 +126,13 @@ int d1_wait_init(void *worlds, int n, int count, const D1Config *cfg, const D1Wa
 int d1_wait_run(void *worlds, int n, int count, const D1Config *cfg, const D1WaitMap *map, int steps,
                 uint32_t *trace, void *stream);
 
+/* Map compiler's LOS flattening (gpu-d1/scripts/compile_corpus.py:56-93,
+ * gpu-d1/scripts/compile_fixture.py:31-48): for each of n_maps byte maps floor[m*5600+p],
+ * los[(m*5600 + origin)*10 + w] gets the 17x17 bitset (bit (dy+8)*17+dx+8) of cells seen
+ * from `origin` by the ray table in `rays` (ray_slots/nslots; floor/cells unused). This
+ * is the `los` table of the learning-task library (include/d1learn.h). */
+int d1_los_table(const uint8_t *floor, int n_maps, const D1Tables *rays, uint32_t *los, void *stream);
+
 /* Categorical sampling with the counter RNG; replaces torch.distributions.Categorical
  * sample/log_prob in the rollout (gpu-d1/scripts/run_ring_ablations.py:350-351).
  * logits: float [n, k] (row stride `ld` floats), 1 <= k <= 64. For env i the uniform

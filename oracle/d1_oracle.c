@@ -115,6 +115,13 @@ static int rng_round(ORng *g, int n, int d) {
     return n / d + (rem && rng_r(g, d) < rem);
 }
 
+/* Exported for the learn-task restatement (oracle/learn_oracle.c). */
+uint32_t o_rng_next(ORng *g) { return rng_next(g); }
+int o_rng_r(ORng *g, int bound) { return rng_r(g, bound); }
+int o_rng_avg(ORng *g, int n) { return rng_avg(g, n); }
+int o_rng_round(ORng *g, int n, int d) { return rng_round(g, n, d); }
+void o_pcg_seed(ORng *g, uint64_t s, uint64_t seq) { pcg_seed(g, s, seq); }
+
 void o_rng_ops(int mode, uint64_t seed, uint64_t seq, int nops, const int32_t *ops,
                const int32_t *args, int32_t *results, uint64_t *final_state) {
     ORng g;

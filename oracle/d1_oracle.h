@@ -40,10 +40,32 @@ typedef struct OState {
     int16_t cells[O_N];
 } OState;
 
+/* One world of the d1-stairs-v2 learning task, the fields of the reference's
+ * learn::State (gpu-d1/branches/d1-stairs-v2/src/learn.cu:113-142) that the task
+ * with 24 enemies and no ogres reads. `error` records a reset that the reference
+ * would stop with an assert (no clump anchor or stair cell). */
+#define O_LE 40
+typedef struct LState {
+    ORng rng;
+    int32_t map_id, player, hp, regen, blocks, ticks, killed, decisions, episode;
+    int32_t next_slot, floor_seen, first_stair_tick, placement_clumped, frontier_count, error;
+    int32_t stairs[3];
+    int16_t pos[O_LE], energy[O_LE], mhp[O_LE], awake[O_LE], enemy_slot[O_LE];
+    uint8_t encountered[O_LE];
+    int16_t occ[O_N];
+    uint8_t seen[O_N], viewed[O_N];
+    int16_t frontier_cells[O_N], frontier_slot[O_N];
+} LState;
+
 #ifdef __cplusplus
 extern "C" {
 #endif
 uint64_t o_mix(uint64_t x);
+uint32_t o_rng_next(ORng *g);
+int o_rng_r(ORng *g, int bound);
+int o_rng_avg(ORng *g, int n);
+int o_rng_round(ORng *g, int n, int d);
+void o_pcg_seed(ORng *g, uint64_t s, uint64_t seq);
 void o_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 void o_set_rays(int nrays, const int8_t *ends_xy, const uint64_t *masks);
 void o_los_bitset(const uint8_t *floor, int origin, uint32_t out[10]);
@@ -63,6 +85,31 @@ void o_rng_ops(int mode, uint64_t seed, uint64_t seq, int nops, const int32_t *o
 int o_wait_run(int count, int steps, int heap, int scenario_fixture, uint64_t seed, uint32_t world,
                const uint8_t *floor, const uint16_t *dist, const int16_t *starts,
                const int32_t *cfg11, const int32_t *kinds24, int32_t prewarm, int32_t *trace);
+
+/* learn-task restatement (oracle/learn_oracle.c); tables hold host pointers */
+struct D1LConfig;
+struct D1LTables;
+int lo_state_bytes(void);
+int lo_field_offset(int k);
+int lo_init(LState *st, int n, const struct D1LConfig *c, const struct D1LTables *t, uint64_t seed, float *obs,
+            float *mask, int clump, int threads);
+int lo_step(LState *st, int n, const struct D1LConfig *c, const struct D1LTables *t, const int64_t *actions, int limit,
+            float *obs, float *mask, float *out, const uint8_t *active, int clump, int threads);
+int lo_heuristic(LState *st, int n, const struct D1LConfig *c, const struct D1LTables *t, int64_t *actions,
+                 int threads);
+void lo_reset(LState *s, const struct D1LConfig *c, const struct D1LTables *t, int clump);
+int lo_reveal(LState *s, const struct D1LTables *t);
+void lo_refresh_frontier(LState *s, const struct D1LTables *t, int p);
+void lo_observe(LState *s, const struct D1LConfig *c, const struct D1LTables *t, float *obs, float *mask);
+void lo_known_distances(const LState *s, const struct D1LTables *t, uint16_t *ds, int nearest_only);
+int lo_route_first_step(int player, int target, const uint16_t *ds);
+int lo_nearest_stair(const LState *s, const uint16_t *ds);
+int lo_in_view(const LState *s, const struct D1LTables *t, int p);
+void lo_transition(LState *s, const struct D1LConfig *c, const struct D1LTables *t, int action, int limit,
+                   float *out, int clump);
+int lo_heuristic_one(LState *s, const struct D1LConfig *c, const struct D1LTables *t);
+void lo_distance_table(const uint8_t *floor, const int16_t *cells, int ncells, uint16_t *out);
+void lo_los_table(const uint8_t *floor, uint32_t *out);
 #ifdef __cplusplus
 }
 #endif

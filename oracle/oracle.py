@@ -111,3 +111,127 @@ def philox(ctr, key):
     o = np.zeros(4, np.uint32)
     lib().o_philox(c.ctypes.data, k.ctypes.data, o.ctypes.data)
     return o
+
+
+# ---------------------------------------------------------------- learning task (learn_oracle.c)
+_LEARN_READY = False
+
+
+def learn_lib():
+    global _LEARN_READY
+    L = lib()
+    if not _LEARN_READY:
+        p, i = C.c_void_p, C.c_int
+        L.lo_state_bytes.argtypes = []
+        L.lo_field_offset.argtypes = [i]
+        L.lo_init.argtypes = [p, i, p, p, C.c_uint64, p, p, i, i]
+        L.lo_step.argtypes = [p, i, p, p, p, i, p, p, p, p, i, i]
+        L.lo_heuristic.argtypes = [p, i, p, p, p, i]
+        L.lo_reset.argtypes = [p, p, p, i]
+        L.lo_reveal.argtypes = [p, p]
+        L.lo_refresh_frontier.argtypes = [p, p, i]
+        L.lo_observe.argtypes = [p, p, p, p, p]
+        L.lo_known_distances.argtypes = [p, p, p, i]
+        L.lo_route_first_step.argtypes = [i, i, p]
+        L.lo_nearest_stair.argtypes = [p, p]
+        L.lo_in_view.argtypes = [p, p, i]
+        L.lo_transition.argtypes = [p, p, p, i, i, p, i]
+        L.lo_heuristic_one.argtypes = [p, p, p]
+        L.lo_distance_table.argtypes = [p, p, i, p]
+        L.lo_los_table.argtypes = [p, p]
+        _LEARN_READY = True
+    return L
+
+
+class LearnTablesHost:
+    """Host tables as the reference's wrappers build them: byte floor, row-major floor
+    cells padded with -1, cell index, all-pairs floor BFS rows, LOS bitsets
+    (gpu-d1/scripts/compile_corpus.py:18-93; learn_env_ring_multi.py:68-86)."""
+
+    def __init__(self, floors, los=None):
+        L = learn_lib()
+        floors = np.ascontiguousarray(np.asarray(floors, np.uint8).reshape(-1, 5600))
+        M = len(floors)
+        self.floor = floors.reshape(-1).copy()
+        self.cells = np.full(M * 5600, -1, np.int16)
+        self.index = np.full(M * 5600, -1, np.int16)
+        self.ncells = np.zeros(M, np.int32)
+        rows = []
+        for m, f in enumerate(floors):
+            c = np.flatnonzero(f).astype(np.int16)
+            self.cells[m * 5600:m * 5600 + len(c)] = c
+            self.index[m * 5600 + c] = np.arange(len(c), dtype=np.int16)
+            self.ncells[m] = len(c)
+            d = np.empty((len(c), 5600), np.uint16)
+            L.lo_distance_table(f.ctypes.data, c.ctypes.data, len(c), d.ctypes.data)
+            rows.append(d)
+        self.distance = np.ascontiguousarray(np.concatenate(rows))
+        self.offsets = np.concatenate(([0], np.cumsum(self.ncells[:-1]))).astype(np.int32)
+        if los is None:
+            los = np.zeros((M, 5600, 10), np.uint32)
+            for m, f in enumerate(floors):
+                L.lo_los_table(np.ascontiguousarray(f).ctypes.data, los[m].ctypes.data)
+        self.los = np.ascontiguousarray(los, np.uint32)
+        self.n_maps = M
+
+    def tables(self, map_filter=-1):
+        return pkg.config.D1LTables(self.floor.ctypes.data, self.cells.ctypes.data, self.index.ctypes.data,
+                                    self.distance.ctypes.data, int(self.ncells[0]), self.ncells.ctypes.data,
+                                    self.offsets.ctypes.data, self.n_maps, map_filter, self.los.ctypes.data)
+
+
+def lstate_dtype():
+    L = learn_lib()
+    off = [L.lo_field_offset(k) for k in range(15)]
+    names = ['rng', 'scalars', 'stairs', 'pos', 'energy', 'mhp', 'awake', 'enemy_slot', 'encountered', 'occ', 'seen',
+             'viewed', 'frontier_cells', 'frontier_slot']
+    formats = [('u1', 48), ('<i4', 15), ('<i4', 3), ('<i2', 40), ('<i2', 40), ('<i2', 40), ('<i2', 40), ('<i2', 40),
+               ('u1', 40), ('<i2', 5600), ('u1', 5600), ('u1', 5600), ('<i2', 5600), ('<i2', 5600)]
+    return np.dtype({'names': names, 'formats': formats, 'offsets': off[:14], 'itemsize': off[14]})
+
+
+SCALARS = ('map_id', 'player', 'hp', 'regen', 'blocks', 'ticks', 'killed', 'decisions', 'episode', 'next_slot',
+           'floor_seen', 'first_stair_tick', 'placement_clumped', 'frontier_count', 'error')
+
+
+class OracleLearn:
+    """Batch of d1-stairs-v2 worlds stepped by the CPU restatement; numpy buffers mirror
+    dcss-auto_amd.learn.LearnEnv."""
+
+    def __init__(self, batch, maps, seed=0, clump=0, map_filter=-1, limit=2048, threads=1):
+        self.L, self.batch, self.maps, self.clump = learn_lib(), batch, maps, clump
+        self.limit, self.threads = limit, threads
+        self.tab = maps.tables(map_filter)
+        self.cfg = pkg.config.learn_config()
+        self.dtype = lstate_dtype()
+        self.state = np.zeros(batch * self.dtype.itemsize, np.uint8)
+        self.obs = np.zeros((batch, 1015), np.float32)
+        self.mask = np.zeros((batch, 19), np.float32)
+        self.out = np.zeros((batch, 45), np.float32)
+        self.reset(seed)
+
+    def reset(self, seed):
+        return self.L.lo_init(ptr(self.state), self.batch, C.byref(self.cfg), C.byref(self.tab), seed, ptr(self.obs),
+                              ptr(self.mask), self.clump, self.threads)
+
+    def step(self, actions, active=None):
+        a = np.ascontiguousarray(actions, np.int64)
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        return self.L.lo_step(ptr(self.state), self.batch, C.byref(self.cfg), C.byref(self.tab), ptr(a), self.limit,
+                              ptr(self.obs), ptr(self.mask), ptr(self.out), ptr(act), self.clump, self.threads)
+
+    def heuristic(self):
+        a = np.zeros(self.batch, np.int64)
+        self.L.lo_heuristic(ptr(self.state), self.batch, C.byref(self.cfg), C.byref(self.tab), ptr(a), self.threads)
+        return a
+
+    def fields(self):
+        """Writable structured view of the worlds (LState, oracle/d1_oracle.h)."""
+        return self.state.view(self.dtype)
+
+    def scalar(self, name):
+        return self.fields()['scalars'][:, SCALARS.index(name)]
+
+    def world(self, i):
+        """Pointer to world i (for the single-world hooks)."""
+        return self.state.ctypes.data + i * self.dtype.itemsize

@@ -1,4 +1,5 @@
-"""The C-ABI library loads and exports every symbol include/d1hip.h declares (no GPU needed)."""
+"""The C-ABI libraries load and export every symbol include/d1hip.h and include/d1learn.h
+declare (no GPU needed)."""
 import ctypes as C
 import re
 
@@ -7,9 +8,9 @@ import pytest
 from conftest import ROOT
 
 
-def declared_symbols():
-    text = (ROOT / 'include' / 'd1hip.h').read_text()
-    return sorted(set(re.findall(r'^\w[\w\s\*]*?\b(d1_\w+)\s*\(', text, re.M)))
+def declared_symbols(header='d1hip.h', prefix='d1_'):
+    text = (ROOT / 'include' / header).read_text()
+    return sorted(set(re.findall(r'^\w[\w\s\*]*?\b(' + prefix + r'\w+)\s*\(', text, re.M)))
 
 
 def test_header_declares_the_abi():
@@ -18,7 +19,41 @@ def test_header_declares_the_abi():
                                          'd1_obs_to_bf16', 'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd',
                                          'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
                                          'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
-                                         'd1_sample_ar'])
+                                         'd1_sample_ar', 'd1_los_table'])
+    # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
+    assert declared_symbols('d1learn.h', 'learn_') == sorted(
+        ['learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size', 'learn_action_size',
+         'learn_out_size', 'learn_config_bytes', 'learn_init', 'learn_step', 'learn_step_active',
+         'learn_heuristic'])
+
+
+@pytest.mark.parametrize('clump', [0, 1])
+def test_learn_library_exports(pkg, clump):
+    import importlib
+    _lib = importlib.import_module('dcss-auto_amd._lib')
+    lib = _lib.load_learn(clump)
+    for name in declared_symbols('d1learn.h', 'learn_'):
+        assert hasattr(lib, name), name
+    assert sorted(_lib.LEARN_SYMBOLS) == declared_symbols('d1learn.h', 'learn_')
+    assert (lib.learn_obs_size(), lib.learn_action_size(), lib.learn_out_size()) == (1015, 19, 45)
+    assert lib.learn_config_bytes() == C.sizeof(pkg.config.D1LConfig) == 140
+    assert lib.learn_state_bytes() == 13184
+    assert lib.learn_turn_cost() == pytest.approx(1e-5) and lib.learn_return_gamma() == 1.0
+    cfg = pkg.config.learn_config()
+    tab = pkg.config.D1LTables(1, 1, None, None, 836, 1, None, 1, -1, 1)
+    assert lib.learn_init(1, 4, C.byref(cfg), C.byref(tab), 0, None, None, None, 0) == -3   # no host path
+    assert lib.learn_init(1, 4, C.byref(pkg.config.learn_config(23)), C.byref(tab), 0, None, None, None, 1) == -2
+    nolos = pkg.config.D1LTables(1, 1, None, None, 836, 1, None, 1, -1, None)
+    assert lib.learn_step(1, 4, C.byref(cfg), C.byref(nolos), 1, 2048, None, None, None, None, 1) == -1
+    assert lib.learn_step(1, 0, C.byref(cfg), C.byref(tab), 1, 2048, None, None, None, None, 1) == 0
+
+
+def test_learn_config_packing(pkg):
+    """The reference wrapper's int array (learn_env_ring_multi.py:93-97) and the struct agree."""
+    cfg = pkg.config.learn_config()
+    words = list((C.c_int32 * 35).from_buffer_copy(bytes(cfg)))
+    assert words[:11] == [24, 3631, 18, 681, 794, 906, 2, 23, 1, 25, 26]   # gdr: 393216^(1/4), 458752^(1/4)
+    assert words[11:15] == [10, 3, 19, 15]
 
 
 def test_library_exports_declared_symbols(pkg):

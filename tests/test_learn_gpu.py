@@ -1,0 +1,129 @@
+"""GPU parity of the learn_* drop-in (libd1learn_clump{0,1}.so) against the CPU
+restatement (oracle/learn_oracle.c): every step, bit for bit, the fp32 observation,
+the mask, the 45 outcome fields, the controller's actions and the world state
+(RNG, player, enemies, memory bitmap, frontier-list order)."""
+import ctypes as C
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+W, N = 80, 5600
+
+
+@pytest.fixture(scope='module')
+def L():
+    return importlib.import_module('dcss-auto_amd.learn')
+
+
+@pytest.fixture(scope='module')
+def O():
+    from oracle import oracle
+    oracle.learn_lib()
+    return oracle
+
+
+def gen_floors(O, k, seed=11):
+    return [O.level(seed, e) for e in range(k)]
+
+
+def compare_state(L, O, gpu_env, ref, step):
+    g = L.decode_rows(gpu_env.state.cpu().numpy())
+    r = ref.fields()
+    names = {'player': 'player', 'hp': 'hp', 'regen': 'regen', 'blocks': 'blocks', 'ticks': 'ticks',
+             'killed': 'killed', 'decisions': 'decisions', 'floor_seen': 'floor_seen', 'episode': 'episode',
+             'first_stair_tick': 'first_stair_tick', 'map_id': 'map_id', 'next_slot': 'next_slot',
+             'frontier_count': 'frontier_count', 'clumped': 'placement_clumped', 'error': 'error'}
+    for gk, rk in names.items():
+        np.testing.assert_array_equal(g[gk], ref.scalar(rk), err_msg=f'{gk} at step {step}')
+    np.testing.assert_array_equal(g['stairs'], r['stairs'], err_msg=f'stairs at step {step}')
+    np.testing.assert_array_equal(g['rng_state'], r['rng'][:, :8].copy().view(np.uint64)[:, 0],
+                                  err_msg=f'rng at step {step}')
+    for gk, rk in (('pos', 'pos'), ('hp', 'mhp'), ('energy', 'energy'), ('awake', 'awake'), ('slot', 'enemy_slot')):
+        np.testing.assert_array_equal(g['mon'][gk], r[rk][:, :24], err_msg=f'enemy {gk} at step {step}')
+    enc = (g['encountered'][:, None] >> np.arange(24, dtype=np.uint64)) & 1
+    np.testing.assert_array_equal(enc, r['encountered'][:, :24], err_msg=f'encountered at step {step}')
+    for i in range(len(g)):
+        assert np.array_equal(L.bitmap_cells(g['viewed'][i]), r['viewed'][i].astype(bool)), f'viewed env {i} step {step}'
+        n = int(g['frontier_count'][i])
+        assert np.array_equal(g['frontier'][i][:n], r['frontier_cells'][i][:n].astype(np.uint16)), \
+            f'frontier list env {i} step {step}'
+
+
+def run_parity(L, O, floors, batch, steps, seed, clump, map_filter, check_state_every=1):
+    maps = L.LearnMaps(np.stack(floors))
+    host = O.LearnTablesHost(np.stack(floors))
+    assert np.array_equal(maps.los.cpu().numpy().view(np.uint32), host.los), 'LOS tables differ'
+    env = L.LearnEnv(batch, seed=seed, maps=maps, map_filter=map_filter, clump=clump)
+    ref = O.OracleLearn(batch, host, seed=seed, clump=clump, map_filter=map_filter, threads=8)
+    rng = np.random.default_rng(seed)
+    torch.cuda.synchronize()
+    for step in range(steps):
+        print(f'learn parity clump={clump} maps={len(floors)} step {step}', flush=True)
+        assert np.array_equal(env.obs.cpu().numpy().view(np.uint32), ref.obs.view(np.uint32)), f'obs at step {step}'
+        assert np.array_equal(env.mask.cpu().numpy(), ref.mask), f'mask at step {step}'
+        if step % check_state_every == 0:
+            compare_state(L, O, env, ref, step)
+        h = ref.heuristic()
+        assert np.array_equal(env.heuristic().cpu().numpy(), h), f'heuristic at step {step}'
+        if step % 3 == 2:   # mix in random (also invalid) actions
+            a = rng.integers(-1, 21, batch).astype(np.int64)
+        else:
+            a = h
+        env.step(torch.from_numpy(a).cuda())
+        assert ref.step(a) == 0
+        assert np.array_equal(env.out.cpu().numpy().view(np.uint32), ref.out.view(np.uint32)), f'out at step {step}'
+    compare_state(L, O, env, ref, steps)
+    return env, ref
+
+
+def test_los_compiler_matches_fixture(L, golden):
+    maps = L.LearnMaps()
+    torch.cuda.synchronize()
+    assert np.array_equal(maps.los[0].cpu().numpy().view(np.uint32), np.load(golden / 'map1057_los.npz')['los'])
+
+
+def test_parity_map1057(L, O):
+    env, ref = run_parity(L, O, [O.pkg.data.map1057()['floor']], batch=48, steps=300, seed=471, clump=0,
+                          map_filter=-1)
+    assert ref.scalar('episode').sum() > 0   # some episodes ended and reset inside the run
+
+
+def test_parity_multimap_clumped(L, O):
+    floors = [O.pkg.data.map1057()['floor']] + gen_floors(O, 3)
+    env, ref = run_parity(L, O, floors, batch=48, steps=240, seed=5, clump=1, map_filter=-2, check_state_every=4)
+    assert len(set(ref.scalar('map_id').tolist())) > 1
+    assert ref.scalar('placement_clumped').any()
+
+
+def test_active_mask_freezes_worlds(L, O):
+    env = L.LearnEnv(32, seed=3)
+    ref = O.OracleLearn(32, O.LearnTablesHost(O.pkg.data.map1057()['floor'][None]), seed=3)
+    rng = np.random.default_rng(0)
+    for step in range(40):
+        active = rng.random(32) < 0.6
+        a = ref.heuristic()
+        before_state = env.state.clone()
+        before_obs, before_out = env.obs.clone(), env.out.clone()
+        env.step(torch.from_numpy(a).cuda(), torch.from_numpy(active).cuda())
+        ref.step(a, active)
+        frozen = torch.from_numpy(~active).cuda()
+        assert torch.equal(env.state[frozen], before_state[frozen])
+        assert torch.equal(env.obs[frozen], before_obs[frozen]) and torch.equal(env.out[frozen], before_out[frozen])
+        assert np.array_equal(env.obs.cpu().numpy().view(np.uint32), ref.obs.view(np.uint32)), f'obs {step}'
+
+
+def test_error_codes(L, pkg):
+    env = L.LearnEnv(4, seed=1)
+    lib = env.lib
+    args = (env.state.data_ptr(), 4, C.byref(env.config), C.byref(env.tables), 1, env.obs.data_ptr(),
+            env.mask.data_ptr(), env.stream)
+    assert lib.learn_init(*args, 0) == -3            # no host path
+    bad = pkg.config.learn_config(23)
+    assert lib.learn_init(env.state.data_ptr(), 4, C.byref(bad), C.byref(env.tables), 1, env.obs.data_ptr(),
+                          env.mask.data_ptr(), env.stream, 1) == -2
+    assert lib.learn_turn_cost() == np.float32(1e-5) and lib.learn_return_gamma() == 1.0
+    assert (lib.learn_obs_size(), lib.learn_action_size(), lib.learn_out_size(), lib.learn_config_bytes()) == \
+        (1015, 19, 45, 140)
