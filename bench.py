@@ -177,6 +177,69 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
                          'avg_launch_ms': step_ms}}
 
 
+# Algorithmic bytes of one learning-task decision (k_learn_step): fp32 observation 4060 +
+# mask 76 + outcome 180 + action 8 + 2 x (80 header + 192 enemies) + 2 x 840 memory
+# bitmap + 840 floor bitmap; the frontier list (2 bytes per anchor read, changed
+# entries written) is left out.
+LEARN_STEP_BYTES = 4060 + 76 + 180 + 8 + 2 * 272 + 2 * 840 + 840
+
+
+def learn_cpu_baseline(envs=4096, steps=500, threads=None):
+    """The learning-task restatement (oracle/learn_oracle.c, OpenMP over worlds) on map
+    1057 with the controller's actions."""
+    from oracle import oracle as O
+    pkg = importlib.import_module('dcss-auto_amd')
+    threads = threads or min(16, os.cpu_count() or 1)
+    env = O.OracleLearn(envs, O.LearnTablesHost(pkg.data.map1057()['floor'][None]), seed=1, threads=threads)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        env.step(env.heuristic())
+    dt = time.perf_counter() - t0
+    return {'value': envs * steps / dt, 'unit': 'decisions/s (step+obs+mask+heuristic)', 'cores': threads,
+            'kind': 'port', 'sample': f'{envs} worlds x {steps} heuristic decisions on map 1057, {dt:.2f} s wall'}
+
+
+def learn_bench(args, warmup=8):
+    """The d1-stairs-v2 drop-in (learn_* ABI): N worlds on map 1057 driven by the library's
+    own controller (learn_heuristic), each decision = one learn_step (joint action, REST
+    repeats, monster turns, auto-reset, fp32 observation [1015], mask [19], outcome [45])."""
+    import torch
+    L = importlib.import_module('dcss-auto_amd.learn')
+    n = args.envs
+    env = L.LearnEnv(n, seed=1, clump=1)
+    for _ in range(warmup):
+        env.step(env.heuristic())
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        ev[k][0].record()
+        a = env.heuristic()
+        ev[k][1].record()
+        env.step(a)
+        ev[k][2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    heur_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    step_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    achieved = LEARN_STEP_BYTES * n / (step_ms * 1e-3) / 1e9
+    result = {'metric': 'learning-task decisions/s (d1-stairs-v2 learn_* drop-in, controller actions)',
+              'value': n * args.steps / wall, 'unit': 'decisions/s', 'n_gpus': 1, 'steps': args.steps,
+              'warmup': warmup, 'ms_per_step': wall / args.steps * 1e3, 'higher_is_better': True,
+              'scaling': 'weak', 'vs_baseline': None, 'dtype': 'int16/u8 state, fp32 obs',
+              'data': 'synthetic: map 1057, 24 enemies, clump mode 1',
+              'config': {'workload': 'learn', 'envs': n, 'obs': 'fp32 1015', 'clump': 1},
+              'roofline': {'bound': 'hbm', 'kernel': 'd1::learn::k_learn_step', 'achieved': achieved,
+                           'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS,
+                           'traffic': measured_traffic(ROOT / 'profiles' / 'k_learn_step_learn.md'),
+                           'bytes_per_env_step': LEARN_STEP_BYTES, 'avg_launch_ms': step_ms},
+              'heuristic_ms': heur_ms, 'step_ms': step_ms,
+              'errors': int(env.errors().numel())}
+    if not args.no_cpu_baseline:
+        result['cpu_baseline'] = learn_cpu_baseline()
+    return result
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -185,7 +248,7 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'wait', 'stress'], default='rollout',
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'wait', 'stress', 'learn'], default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
                          'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer')
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
@@ -201,6 +264,9 @@ def main():
         return
     if args.mode == 'stress':
         print(json.dumps(stress_bench(args)), flush=True)
+        return
+    if args.mode == 'learn':
+        print(json.dumps(learn_bench(args)), flush=True)
         return
     pkg = importlib.import_module('dcss-auto_amd')
     policy_mod = importlib.import_module('dcss-auto_amd.policy')
