@@ -104,6 +104,11 @@ __device__ __forceinline__ int select32(uint32_t v, int j) {
     }
     return pos;
 }
+// position of the k-th set bit of a 64-bit mask (k < popcount)
+__device__ __forceinline__ int select64(uint64_t m, int k) {
+    int lo = __popc((uint32_t)m);
+    return k < lo ? select32((uint32_t)m, k) : 32 + select32((uint32_t)(m >> 32), k - lo);
+}
 __device__ __forceinline__ int row_select(Row r, int j) {
     int c0 = __popc(r.a);
     if (j < c0) return select32(r.a, j);
@@ -127,39 +132,80 @@ __device__ __forceinline__ uint64_t mix64(uint64_t x) {   // gpu-d1/src/sim.h:15
 // ---------------------------------------------------------------- RNG (wave-uniform)
 // PCG32 XSH-RR as gpu-d1/src/sim.h:21-60, or Philox4x32-10 where draw k of stream
 // (t, env, domain) is word k%4 of Philox(ctr={k/4, t, env, domain}, key=seed).
+//
+// The stream is consumed through a 64-lane buffer: lane l of `buf` holds draw base+l,
+// refilled 64 draws at a time by one vector computation (PCG by jump-ahead from the
+// table below, Philox one counter per lane), so a draw is one readlane and the refill
+// code exists once per kernel instead of at every draw site.
+
+// PCG jump-ahead: state after j steps = A[j]*s + C[j]*inc (A[j] = a^j, C[j] = sum_{i<j} a^i).
+struct PcgJump {
+    uint64_t a[65], c[65];
+    constexpr PcgJump() : a(), c() {
+        a[0] = 1; c[0] = 0;
+        for (int j = 1; j <= 64; j++) { a[j] = a[j - 1] * 6364136223846793005ULL; c[j] = c[j - 1] * 6364136223846793005ULL + 1; }
+    }
+};
+__constant__ constexpr PcgJump kJump{};
+
+__device__ __forceinline__ uint32_t pcg_out(uint64_t old) {
+    uint32_t x = (uint32_t)(((old >> 18) ^ old) >> 27), r = (uint32_t)(old >> 59);
+    return (x >> r) | (x << ((0u - r) & 31u));
+}
+// PCG32 output of the state `lane` steps after `st`.
+__device__ __noinline__ uint32_t pcg_lane(uint64_t st, uint64_t inc, int lane) {
+    return pcg_out(kJump.a[lane] * st + kJump.c[lane] * inc);
+}
+// Word idx%4 of Philox4x32-10(ctr = {idx/4, t, env, dom}, key = {key0, key1})
+// (Salmon et al., SC'11: multipliers 0xD2511F53/0xCD9E8D57, Weyl increments
+// 0x9E3779B9/0xBB67AE85).
+__device__ __noinline__ uint32_t philox_lane(uint32_t key0, uint32_t key1, uint32_t t, uint32_t env, uint32_t dom,
+                                             uint32_t idx) {
+    uint32_t c0 = idx >> 2, c1 = t, c2 = env, c3 = dom, k0 = key0, k1 = key1;
+#pragma unroll
+    for (int r = 0; r < 10; r++) {
+        uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+        uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+        uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+    }
+    uint32_t j = idx & 3u;
+    return j == 0 ? c0 : j == 1 ? c1 : j == 2 ? c2 : c3;
+}
+
+constexpr uint32_t RNG_EMPTY = 0x80000000u;   // a buffer base no draw index reaches
+
 struct Rng {
-    uint64_t st, inc;
-    uint32_t key0, key1, t, env, dom, k;
-    uint32_t blk;
-    unsigned __int128 buf;   // the current Philox block, word j at bits 32j (no indexed fields)
+    uint64_t st, inc;                   // PCG32: the state before draw `sb`
+    uint32_t key0, key1, t, env, dom;   // counter stream
+    uint32_t k;                         // index of the next draw
+    uint32_t sb, base;                  // PCG state index; draw index held by lane 0
+    uint32_t buf;                       // lane l: draw base + l
     int mode;
 
-    __device__ __forceinline__ void philox_block(uint32_t b) {
-        uint32_t c0 = b, c1 = t, c2 = env, c3 = dom, k0 = key0, k1 = key1;
-#pragma unroll
-        for (int r = 0; r < 10; r++) {
-            uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
-            uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
-            uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-            c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
-            k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+    __device__ __forceinline__ void fill(uint32_t at) {
+        int lane = (int)threadIdx.x;
+        if (mode == 0) {
+            uint32_t j = at - sb;   // <= 64: a fill happens at most 64 draws after the last one
+            st = kJump.a[j] * st + kJump.c[j] * inc;
+            sb = at;
+            buf = pcg_lane(st, inc, lane);
+        } else {
+            buf = philox_lane(key0, key1, t, env, dom, at + (uint32_t)lane);
         }
-        buf = (unsigned __int128)c0 | ((unsigned __int128)c1 << 32) | ((unsigned __int128)c2 << 64) |
-              ((unsigned __int128)c3 << 96);
-        blk = b;
+        base = at;
     }
     __device__ __forceinline__ uint32_t next() {
-        if (mode == 0) {
-            uint64_t old = st;
-            st = old * 6364136223846793005ULL + (inc | 1);
-            uint32_t x = (uint32_t)(((old >> 18) ^ old) >> 27), r = (uint32_t)(old >> 59);
-            return (x >> r) | (x << ((0u - r) & 31u));
-        }
-        uint32_t b = k >> 2;
-        if (b != blk) philox_block(b);
-        uint32_t j = k & 3u;
+        if (k - base >= 64u) fill(k);
+        uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)buf, (int)(k - base));
         k++;
-        return (uint32_t)(buf >> (32 * j));
+        return v;
+    }
+    // PCG32 state before draw k (what the sequential generator would hold now)
+    __device__ __forceinline__ uint64_t pcg_state() const {
+        uint32_t j = k - sb;
+        return kJump.a[j] * st + kJump.c[j] * inc;
     }
     __device__ __forceinline__ int r(int bound) {   // gpu-d1/src/sim.h:36-51
         if (bound <= 1) return 0;
@@ -178,54 +224,36 @@ struct Rng {
     }
     __device__ __forceinline__ int avg(int n) { int a = r(n); return (a + r(n + 1)) / 2; }             // sim.h:52-55
     __device__ __forceinline__ int round(int n, int d) { int rem = n % d; return n / d + (rem && r(d) < rem); }  // sim.h:56-59
-    __device__ __forceinline__ void pcg_seed(uint64_t s, uint64_t seq) {   // sim.h:29-35
-        mode = 0; st = 0; inc = (seq << 1) | 1;
-        next();
-        st += s;
-        next();
+    __device__ __forceinline__ void pcg_load(uint64_t state, uint64_t increment) {
+        mode = 0; st = state; inc = increment; k = 0; sb = 0; base = RNG_EMPTY;
+    }
+    __device__ __forceinline__ void pcg_seed(uint64_t s, uint64_t seq) {   // sim.h:29-35: two steps around +s
+        uint64_t i = (seq << 1) | 1;
+        uint64_t v = i;   // 0 * a + inc
+        v += s;
+        v = v * 6364136223846793005ULL + i;
+        pcg_load(v, i);
     }
     __device__ __forceinline__ void counter(uint64_t key, uint32_t e, uint32_t tt, uint32_t d) {
-        mode = 1; key0 = (uint32_t)key; key1 = (uint32_t)(key >> 32); env = e; t = tt; dom = d; k = 0; blk = 0xFFFFFFFFu;
-        st = 0; inc = 0;
+        mode = 1; key0 = (uint32_t)key; key1 = (uint32_t)(key >> 32); env = e; t = tt; dom = d;
+        k = 0; sb = 0; base = RNG_EMPTY; st = 0; inc = 0;
     }
 };
 
-// PCG jump-ahead: state after j steps = A[j]*s + C[j]*inc (A[j] = a^j, C[j] = sum_{i<j} a^i).
-struct PcgJump {
-    uint64_t a[65], c[65];
-    constexpr PcgJump() : a(), c() {
-        a[0] = 1; c[0] = 0;
-        for (int j = 1; j <= 64; j++) { a[j] = a[j - 1] * 6364136223846793005ULL; c[j] = c[j - 1] * 6364136223846793005ULL + 1; }
-    }
-};
-__constant__ constexpr PcgJump kJump{};
-
-__device__ __forceinline__ uint32_t pcg_out(uint64_t old) {
-    uint32_t x = (uint32_t)(((old >> 18) ^ old) >> 27), r = (uint32_t)(old >> 59);
-    return (x >> r) | (x << ((0u - r) & 31u));
-}
 // Reservoir choice over `total` eligible cells: the 1-based count c is kept when
 // r(c) == 0, the last kept count wins (gpu-d1/branches/d1-stairs-v2/src/learn.cu:432-441).
 // 64 counts per pass: lane l evaluates count c0+l from the draw it would get if no
-// earlier draw in the pass were rejected; a pass in which any Lemire rejection is
-// possible (low < bound) is replayed serially, so the draw sequence is the serial one.
+// earlier draw in the pass were rejected (the buffer refilled at the current index);
+// a pass in which any Lemire rejection is possible (low < bound) is replayed serially,
+// so the draw sequence is the serial one.
 __device__ __forceinline__ int reservoir(Rng &s, int total, int lane) {
     int chosen = total >= 1 ? 0 : -1;
     int c0 = 2;
     while (c0 <= total) {
         int cnt = imin(64, total - c0 + 1);
         int c = c0 + lane;
-        uint32_t xw;
-        if (s.mode == 0) {
-            uint64_t old = kJump.a[lane] * s.st + kJump.c[lane] * s.inc;
-            xw = pcg_out(old);
-        } else {
-            uint32_t kk = s.k + (uint32_t)lane;
-            Rng tmp = s;
-            tmp.philox_block(kk >> 2);
-            xw = (uint32_t)(tmp.buf >> (32 * (kk & 3u)));
-        }
-        uint64_t m = (uint64_t)xw * (uint32_t)c;
+        if (s.base != s.k) s.fill(s.k);
+        uint64_t m = (uint64_t)s.buf * (uint32_t)c;
         bool act = lane < cnt;
         bool risky = act && (uint32_t)m < (uint32_t)c;
         if (ballot(risky)) {
@@ -233,8 +261,7 @@ __device__ __forceinline__ int reservoir(Rng &s, int total, int lane) {
         } else {
             uint64_t keep = ballot(act && (m >> 32) == 0);
             if (keep) chosen = c0 + 63 - __clzll((long long)keep) - 1;
-            if (s.mode == 0) s.st = kJump.a[cnt] * s.st + kJump.c[cnt] * s.inc;
-            else s.k += (uint32_t)cnt;
+            s.k += (uint32_t)cnt;
         }
         c0 += cnt;
     }
@@ -458,37 +485,55 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p) {
     int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
     int q = nbr(p, d);
     bool ok = x.lane < 8 && walkable(x, q);
-    int rel = ok ? rel_dist(x, q, p) : BIG;
-    uint64_t okm = ballot(ok);
-    int best = -1, bd = 0, ties = 0;
-    for (int zz = 0; zz < 8; zz++) {
-        if (!((okm >> zz) & 1)) continue;
-        int dd = lane_val(rel, zz), qq = lane_val(q, zz);
-        if (dd < bd) { bd = dd; best = qq; ties = 1; }
-        else if (dd == bd && best >= 0 && x.g.r(++ties) == 0) best = qq;
-    }
-    if (best >= 0 || !x.c->repair) return best;
-    // queue: lane j holds cells[j] and first[j]
-    int qcell = x.lane == 0 ? p : -1, qfirst = -1, len = 1;
-    for (int head = 0; head < len; head++) {
-        int cell = lane_val(qcell, head);
-        int hfirst = lane_val(qfirst, head);
-        int nq = nbr(cell, x.lane & 7);
-        bool v = x.lane < 8 && walkable(x, nq);
-        uint64_t vm = ballot(v);
-        for (int dd = 0; dd < 8; dd++) {
-            if (!((vm >> dd) & 1)) continue;
-            int qq = lane_val(nq, dd);
-            if (ballot(x.lane < len && qcell == qq)) continue;
-            int step = head == 0 ? qq : hfirst;
-            if (rel_dist(x, qq, p) < 0) return step;
-            if (len < 24) {
-                if (x.lane == len) { qcell = qq; qfirst = step; }
-                len++;
-            }
+    // Reached neighbours differ from p by at most one layer, so only the lower ones
+    // (rel -1) can be chosen: the first in rotated order is taken, each later one
+    // replaces it when r(++ties) == 0. Equal and higher ones neither win nor draw.
+    uint64_t low = ballot(ok && rel_dist(x, q, p) < 0);
+    if (low) {
+        int best = lane_val(q, __ffsll((unsigned long long)low) - 1), ties = 1;
+        for (low &= low - 1; low; low &= low - 1) {
+            int qq = lane_val(q, __ffsll((unsigned long long)low) - 1);
+            if (x.g.r(++ties) == 0) best = qq;
         }
+        return best;
     }
-    return -1;
+    if (!x.c->repair) return -1;
+    // Bounded 24-node BFS detour. Lanes 0..23 hold the queue (cell, first step);
+    // each head expands its 8 directions at once: sm->front marks queued cells, the
+    // first lower candidate in direction order returns, otherwise the new candidates
+    // are appended in direction order while the queue has room.
+    Smem *sm = x.sm;
+    int qcell = x.lane == 0 ? p : -1, qfirst = -1, len = 1, result = -1;
+    if (x.lane == 0) atomicOr(&sm->front[(p / W) * RW + ((p % W) >> 5)], 1u << ((p % W) & 31));
+    __syncthreads();
+    for (int head = 0; head < len; head++) {
+        int cell = lane_val(qcell, head), hfirst = lane_val(qfirst, head);
+        int nq = nbr(cell, x.lane & 7);
+        bool v = x.lane < 8 && walkable(x, nq) && !bit(sm->front, nq);
+        uint64_t vm = ballot(v);
+        if (!vm) continue;
+        int step = head == 0 ? nq : hfirst;
+        uint64_t lm = ballot(v && rel_dist(x, nq, p) < 0);
+        if (lm) {
+            result = lane_val(step, __ffsll((unsigned long long)lm) - 1);
+            break;
+        }
+        int cnt = imin(__popcll(vm), 24 - len);
+        if (cnt <= 0) continue;
+        int k = x.lane - len;
+        bool take = k >= 0 && k < cnt;
+        int src = take ? select64(vm, k) : 0;
+        int cq = __shfl(nq, src), cf = __shfl(step, src);
+        if (take) { qcell = cq; qfirst = cf; }
+        if (v && __popcll(vm & ((1ULL << x.lane) - 1ULL)) < cnt)
+            atomicOr(&sm->front[(nq / W) * RW + ((nq % W) >> 5)], 1u << ((nq % W) & 31));
+        len += cnt;
+        __syncthreads();
+    }
+    if (x.lane < len)
+        atomicAnd(&sm->front[(qcell / W) * RW + ((qcell % W) >> 5)], ~(1u << ((qcell % W) & 31)));
+    __syncthreads();
+    return result;
 }
 // One BFS layer for row y: dilate the frontier rows y-1..y+1 by one cell, keep floor
 // cells not reached yet.
@@ -542,6 +587,9 @@ __device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
         }
         if (layer >= stop) break;
     }
+    __syncthreads();
+    for (int w = x.lane; w < ROWS_WORDS; w += 64) sm->front[w] = 0;   // the repair BFS's queued-cell marks
+    __syncthreads();
 }
 // gpu-d1/src/sim.h:254-269
 __device__ __forceinline__ void act(Ctx &x, int id) {

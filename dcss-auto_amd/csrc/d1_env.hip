@@ -275,7 +275,7 @@ __device__ __forceinline__ uint32_t state_hash(Ctx &x) {
     uint32_t scal = term((uint32_t)x.player, 0) + term((uint32_t)x.hp, 1) + term((uint32_t)x.regen, 2) +
                     term((uint32_t)x.ticks, 3) + term((uint32_t)x.killed, 4) + term((uint32_t)x.decisions, 5) +
                     term((uint32_t)x.floor_seen, 6) + term((uint32_t)x.episode, 7) +
-                    term(x.g.mode == 0 ? (uint32_t)x.g.st : 0u, 8) + term(x.g.mode == 0 ? (uint32_t)(x.g.st >> 32) : 0u, 9) +
+                    term(x.g.mode == 0 ? (uint32_t)x.g.pcg_state() : 0u, 8) + term(x.g.mode == 0 ? (uint32_t)(x.g.pcg_state() >> 32) : 0u, 9) +
                     term(x.t, 10) + term((uint32_t)stair_at(x, 0), 11) + term((uint32_t)stair_at(x, 1), 12) +
                     term((uint32_t)stair_at(x, 2), 13) + term((uint32_t)x.first_stair_tick, 14);
     uint32_t h = x.lane == 0 ? scal : 0u;
@@ -296,7 +296,7 @@ __device__ __forceinline__ void load_world(Ctx &x, const uint8_t *row, int max_m
     x.episode = h.episode; x.first_stair_tick = h.first_stair_tick;
     x.stairs = pack_stairs(h.stairs[0], h.stairs[1], h.stairs[2]);
     x.blocks = h.blocks; x.t = h.t; x.env_id = h.env_id;
-    if (x.c->rng_mode == 0) { x.g.mode = 0; x.g.st = h.rng_state; x.g.inc = h.rng_inc; }
+    if (x.c->rng_mode == 0) x.g.pcg_load(h.rng_state, h.rng_inc);
     else x.g.counter(h.rng_state, h.env_id, h.t, 0);
     Mon m{-1, 0, -30000, 0, 0};
     if (x.lane < max_m) m = ((const Mon *)(row + 64))[x.lane];
@@ -312,7 +312,7 @@ __device__ __forceinline__ void load_world(Ctx &x, const uint8_t *row, int max_m
 __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
     if (x.lane == 0) {
         Hdr h;
-        h.rng_state = x.g.mode == 0 ? x.g.st : ((uint64_t)x.g.key1 << 32 | x.g.key0);
+        h.rng_state = x.g.mode == 0 ? x.g.pcg_state() : ((uint64_t)x.g.key1 << 32 | x.g.key0);
         h.rng_inc = x.g.mode == 0 ? x.g.inc : 0;
         h.env_id = x.env_id; h.t = x.t; h.episode = x.episode;
         h.player = (int16_t)x.player; h.hp = (int16_t)x.hp; h.regen = (int16_t)x.regen; h.ncells = (int16_t)x.ncells;
@@ -479,6 +479,7 @@ __device__ __forceinline__ void wait_stage_map(Ctx &x, const D1WaitMap &map) {
             sm->floor[y * RW + j] = f;
             sm->reach[y * RW + j] = r;
             sm->occ[y * RW + j] = 0;
+            sm->front[y * RW + j] = 0;
         }
     }
     for (int p = x.lane; p < N; p += 64) sm->dist[p] = (uint8_t)map.dist[p];
@@ -517,11 +518,11 @@ __device__ __forceinline__ uint32_t wait_digest(Ctx &x, int count) {
     uint32_t h = x.lane < count ? term((uint16_t)x.mpos | (uint32_t)(uint16_t)x.menergy << 16, 100 + x.lane) : 0u;
     h = wave_sum(h);
     return h + term((uint32_t)x.hp, 0) + term((uint32_t)x.regen, 1) + term((uint32_t)x.blocks, 2) +
-           term((uint32_t)x.episode, 3) + term((uint32_t)x.g.st, 4) + term((uint32_t)(x.g.st >> 32), 5);
+           term((uint32_t)x.episode, 3) + term((uint32_t)x.g.pcg_state(), 4) + term((uint32_t)(x.g.pcg_state() >> 32), 5);
 }
 __device__ __forceinline__ void wait_load(Ctx &x, const uint8_t *row, int count, int &fixture) {
     WaitHdr h = *(const WaitHdr *)row;
-    x.g.mode = 0; x.g.st = h.rng_state; x.g.inc = h.rng_inc;
+    x.g.pcg_load(h.rng_state, h.rng_inc);
     x.hp = h.hp; x.regen = h.regen; x.blocks = h.blocks; x.episode = h.episode; fixture = h.fixture;
     x.mpos = -1; x.menergy = -30000; x.mkind = x.lane % 6; x.mhp = 1; x.mawake = 1;
     if (x.lane < count) {
@@ -534,7 +535,7 @@ __device__ __forceinline__ void wait_load(Ctx &x, const uint8_t *row, int count,
 __device__ __forceinline__ void wait_store(Ctx &x, uint8_t *row, int count, int fixture) {
     if (x.lane == 0) {
         WaitHdr h{};
-        h.rng_state = x.g.st; h.rng_inc = x.g.inc;
+        h.rng_state = x.g.pcg_state(); h.rng_inc = x.g.inc;
         h.hp = x.hp; h.regen = x.regen; h.blocks = x.blocks; h.fixture = fixture; h.episode = x.episode;
         *(WaitHdr *)row = h;
     }

@@ -90,11 +90,6 @@ __device__ __forceinline__ int wave_min(int v) {
 __device__ __forceinline__ int lanes_below(uint64_t m, int lane) {
     return __popcll(m & ((1ULL << lane) - 1ULL));
 }
-// k-th set bit of a 64-bit mask (k < popcount)
-__device__ __forceinline__ int select64(uint64_t m, int k) {
-    int lo = __popc((uint32_t)m);
-    return k < lo ? select32((uint32_t)m, k) : 32 + select32((uint32_t)(m >> 32), k - lo);
-}
 __device__ __forceinline__ bool floor_b(const LCtx &c, int p) { return p >= 0 && bit(c.x.sm->floor, p); }
 
 // ---------------------------------------------------------------- view from the LOS table
@@ -847,7 +842,7 @@ __device__ __forceinline__ int heuristic_learn(LCtx &c) {
 __device__ __forceinline__ void load_learn(LCtx &c, const uint8_t *row, bool list_too) {
     Ctx &x = c.x;
     const LHdr h = *(const LHdr *)row;
-    x.g.mode = 0; x.g.st = h.rng_state; x.g.inc = h.rng_inc;
+    x.g.pcg_load(h.rng_state, h.rng_inc);
     c.enc = h.encountered;
     x.ticks = h.ticks; x.killed = h.killed; x.decisions = h.decisions; x.floor_seen = h.floor_seen;
     x.episode = h.episode; x.first_stair_tick = h.first_stair_tick;
@@ -882,7 +877,7 @@ __device__ __forceinline__ void store_learn(LCtx &c, uint8_t *row) {
     Ctx &x = c.x;
     if (x.lane == 0) {
         LHdr h{};
-        h.rng_state = x.g.st; h.rng_inc = x.g.inc; h.encountered = c.enc;
+        h.rng_state = x.g.pcg_state(); h.rng_inc = x.g.inc; h.encountered = c.enc;
         h.ticks = x.ticks; h.killed = x.killed; h.decisions = x.decisions; h.floor_seen = x.floor_seen;
         h.episode = x.episode; h.first_stair_tick = x.first_stair_tick;
         h.player = (int16_t)x.player; h.hp = (int16_t)x.hp; h.regen = (int16_t)x.regen; h.blocks = (int16_t)x.blocks;
