@@ -279,7 +279,6 @@ struct Ctx {
     uint64_t stairs;   // three int16 cells at bits 0, 16, 32 (-1 = none)
     uint32_t t, env_id;
     uint64_t vis0, vis1, vis2, vis3;   // player view, quadrants (+,+) (-,+) (-,-) (+,-)
-    bool adj_clear;                     // the 8 neighbours of any cell are always in view
     // this lane's monster (lane < count)
     int mpos, mhp, menergy, mawake, mkind;
     int lane;
@@ -506,7 +505,8 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p) {
     int qcell = x.lane == 0 ? p : -1, qfirst = -1, len = 1, result = -1;
     if (x.lane == 0) atomicOr(&sm->front[(p / W) * RW + ((p % W) >> 5)], 1u << ((p % W) & 31));
     __syncthreads();
-    for (int head = 0; head < len; head++) {
+    int head = 0;
+    for (; head < len && len < 24; head++) {
         int cell = lane_val(qcell, head), hfirst = lane_val(qfirst, head);
         int nq = nbr(cell, x.lane & 7);
         bool v = x.lane < 8 && walkable(x, nq) && !bit(sm->front, nq);
@@ -529,6 +529,16 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p) {
             atomicOr(&sm->front[(nq / W) * RW + ((nq % W) >> 5)], 1u << ((nq % W) & 31));
         len += cnt;
         __syncthreads();
+    }
+    // Queue full: nothing more is appended, and a queued cell is never lower, so the
+    // remaining heads only look for the first lower neighbour in (head, direction)
+    // order, eight heads per pass (lane = 8 * head offset + direction).
+    for (; result < 0 && head < len; head += 8) {
+        int h = head + (x.lane >> 3);
+        int cell = __shfl(qcell, imin(h, 23)), hfirst = __shfl(qfirst, imin(h, 23));
+        int nq = nbr(cell, x.lane & 7);
+        uint64_t lm = ballot(h < len && walkable(x, nq) && rel_dist(x, nq, p) < 0);
+        if (lm) result = lane_val(hfirst, __ffsll((unsigned long long)lm) - 1);
     }
     if (x.lane < len)
         atomicAnd(&sm->front[(qcell / W) * RW + ((qcell % W) >> 5)], ~(1u << ((qcell % W) & 31)));

@@ -45,7 +45,10 @@ struct Mon {
 };
 static_assert(sizeof(Mon) == 8, "monster layout");
 
-__host__ __device__ constexpr int off_viewed(int m) { return 64 + 8 * m; }
+// the player's view (4 x u64 quadrant sets) is kept beside the header: it only changes
+// when the player moves, so a step that does not move needs no LOS scan and no reveal
+constexpr int OFF_VIEW = 64, OFF_MON = 96;
+__host__ __device__ constexpr int off_viewed(int m) { return OFF_MON + 8 * m; }
 __host__ __device__ constexpr int off_floor(int m) { return off_viewed(m) + ROWS_WORDS * 4; }
 __host__ __device__ constexpr int off_cells(int m) { return off_floor(m) + ROWS_WORDS * 4; }
 __host__ __device__ constexpr int state_bytes(int m) { return (off_cells(m) + ROWS_WORDS * 4 + 63) / 64 * 64; }
@@ -121,6 +124,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
     const D1Config *c = x.c;
     Smem *sm = x.sm;
     int milli = c->step_milli;
+    bool moved = false;
     x.blocks = 0;
     x.regen += c->regen;
     while (x.regen >= 100) { x.hp = imin(c->hp, x.hp + 1); x.regen -= 100; }
@@ -140,10 +144,13 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
                         milli += c->kill_milli;
                     } else if (x.lane == id) x.mhp = nh;
                 }
-            } else x.player = p;
+            } else {
+                x.player = p;
+                moved = true;
+            }
         }
     }
-    milli += c->explore_milli * reveal(x);
+    if (moved) milli += c->explore_milli * reveal(x);   // an unmoved view reveals nothing new
     saw = visible_awake(x);
     bool clear = (d == 18 && stair_index(x) > 0 && x.hp > 0) || (c->clear_on_kill_all && x.killed == c->count);
     if (!clear) {
@@ -196,7 +203,7 @@ __device__ __forceinline__ void transition(Ctx &x, int action, float *out, const
         int d = 8;
         if (action >= 0 && action < 16) {
             int dir = action % 8, p = nbr(x.player, dir);
-            bool enemy = p >= 0 && (x.adj_clear || in_view(x, p)) && bit(x.sm->occ, p);
+            bool enemy = p >= 0 && in_view(x, p) && bit(x.sm->occ, p);
             bool valid = action < 8 ? p >= 0 && (!bit(x.sm->viewed, p) || bit(x.sm->floor, p)) && !enemy : enemy;
             if (valid) d = dir; else invalid = true;
         } else if (action == 17) invalid = x.hp >= c->hp || visible_awake(x) || c->regen <= 0;
@@ -299,7 +306,9 @@ __device__ __forceinline__ void load_world(Ctx &x, const uint8_t *row, int max_m
     if (x.c->rng_mode == 0) x.g.pcg_load(h.rng_state, h.rng_inc);
     else x.g.counter(h.rng_state, h.env_id, h.t, 0);
     Mon m{-1, 0, -30000, 0, 0};
-    if (x.lane < max_m) m = ((const Mon *)(row + 64))[x.lane];
+    if (x.lane < max_m) m = ((const Mon *)(row + OFF_MON))[x.lane];
+    const uint64_t *vw = (const uint64_t *)(row + OFF_VIEW);
+    x.vis0 = vw[0]; x.vis1 = vw[1]; x.vis2 = vw[2]; x.vis3 = vw[3];
     x.mpos = m.pos; x.mhp = m.hp; x.menergy = m.energy; x.mawake = m.awake; x.mkind = m.kind;
     const uint32_t *vg = (const uint32_t *)(row + off_viewed(max_m));
     const uint32_t *fg = (const uint32_t *)(row + off_floor(max_m));
@@ -325,7 +334,11 @@ __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
         Mon m;
         m.pos = (int16_t)x.mpos; m.hp = (int16_t)x.mhp; m.energy = (int16_t)x.menergy;
         m.awake = (uint8_t)x.mawake; m.kind = (uint8_t)x.mkind;
-        ((Mon *)(row + 64))[x.lane] = m;
+        ((Mon *)(row + OFF_MON))[x.lane] = m;
+    }
+    if (x.lane < 4) {
+        uint64_t v = x.lane == 0 ? x.vis0 : x.lane == 1 ? x.vis1 : x.lane == 2 ? x.vis2 : x.vis3;
+        ((uint64_t *)(row + OFF_VIEW))[x.lane] = v;
     }
     uint32_t *vg = (uint32_t *)(row + off_viewed(max_m));
     for (int w = x.lane; w < ROWS_WORDS; w += 64) vg[w] = x.sm->viewed[w];
@@ -385,7 +398,6 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
     uint8_t *row = state + (size_t)env * row_bytes;
     Ctx x;
     x.sm = &sm; x.c = &cfg; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
-    x.adj_clear = false;
     uint32_t *fg = (uint32_t *)(row + off_floor(max_m));
     uint32_t *cg = (uint32_t *)(row + off_cells(max_m));
     if (cfg.level_mode == 1) {
@@ -433,10 +445,6 @@ __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, s
     const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
     int64_t a = actions[env];
     int action = a < 0 || a > 1000 ? -1 : (int)a;
-    // Adjacent cells are visible whenever their first ray has no blocker (true of the
-    // native table); then only REST needs the full view before the player acts.
-    x.adj_clear = tab.ray_slots[1] == 0 && tab.ray_slots[8] == 0 && tab.ray_slots[9] == 0;
-    if (!x.adj_clear || action == 17) compute_view(x);
     float o8[8];
     transition(x, action, o8, cg);
     x.t++;
@@ -545,7 +553,7 @@ __device__ __forceinline__ void wait_store(Ctx &x, uint8_t *row, int count, int 
     }
 }
 __device__ __forceinline__ void wait_ctx(Ctx &x, Smem *sm, const D1Config *cfg, const D1WaitMap &map) {
-    x.sm = sm; x.c = cfg; x.rays = nullptr; x.nslots = 0; x.lane = lane_id(); x.adj_clear = true;
+    x.sm = sm; x.c = cfg; x.rays = nullptr; x.nslots = 0; x.lane = lane_id();
     x.player = map.player; x.vis0 = x.vis1 = x.vis2 = x.vis3 = 0;
 }
 // scenario 0 contact, 1 approach, 2 mixed (fixture = world % 2, then (world*7)%32 warm-up

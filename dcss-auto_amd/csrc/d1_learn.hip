@@ -904,7 +904,7 @@ __device__ __forceinline__ void store_floor(LCtx &c, uint8_t *row) {
 __device__ __forceinline__ void setup(LCtx &c, LSmem *L, const D1Config *cfg, const D1LTables *t) {
     c.L = L; c.t = t;
     c.x.sm = &L->s; c.x.c = cfg; c.x.rays = nullptr; c.x.nslots = 0; c.x.lane = lane_id();
-    c.x.adj_clear = false; c.x.t = 0; c.x.env_id = 0; c.x.ncells = 0;
+    c.x.t = 0; c.x.env_id = 0; c.x.ncells = 0;
     c.x.vis0 = c.x.vis1 = c.x.vis2 = c.x.vis3 = 0;
     c.clumped = 0; c.error = 0;
 }
