@@ -12,7 +12,7 @@ SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd
            'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16',
            'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd', 'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
            'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
-           'd1_sample_ar', 'd1_los_table')
+           'd1_sample_ar', 'd1_los_table', 'd1_trunk1')
 LEARN_SYMBOLS = ('learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size',
                  'learn_action_size', 'learn_out_size', 'learn_config_bytes', 'learn_init', 'learn_step',
                  'learn_step_active', 'learn_heuristic')
@@ -48,6 +48,7 @@ def load():
                                    C.c_float, p, p]
         L.d1_gae.argtypes = [p, p, p, p, i, i, C.c_float, C.c_float, p, p, p]
         L.d1_los_table.argtypes = [p, i, p, p, p]
+        L.d1_trunk1.argtypes = [p, i, p, p, p, p]
         _LIB = L
     return _LIB
 

@@ -34,7 +34,15 @@ class Policy(nn.Module):
         dtype = self.l1.weight.dtype
         if obs_u8.is_cuda and torch.is_autocast_enabled('cuda'):
             dtype = torch.get_autocast_dtype('cuda')
-        x = widen(obs_u8.reshape(obs_u8.shape[0], -1), dtype)
+        flat = obs_u8.reshape(obs_u8.shape[0], -1)
+        if flat.dtype == torch.uint8 and flat.is_cuda and dtype == torch.bfloat16 and not torch.is_grad_enabled() \
+                and flat.shape[1] == OBS:
+            # layer 1 straight from uint8 (HIP MFMA kernel); layer 2 with bias + ReLU in the hipBLASLt epilogue
+            h = trunk1(flat, self.l1.weight.to(dtype), self.l1.bias.to(dtype))
+            h = torch._addmm_activation(self.l2.bias.to(dtype), h, self.l2.weight.to(dtype).t())
+            out = self.head(h.to(self.head.weight.dtype)).float()
+            return out[:, :self.n_actions], out[:, self.n_actions]
+        x = widen(flat, dtype)
         if x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_grad_enabled():
             # bias + ReLU in the hipBLASLt epilogue
             h = torch._addmm_activation(self.l1.bias, x, self.l1.weight.t())
@@ -44,6 +52,20 @@ class Policy(nn.Module):
             h = torch.relu(self.l2(h))
         out = self.head(h).float()
         return out[:, :self.n_actions], out[:, self.n_actions]
+
+
+def trunk1(obs_u8, w1, b1):
+    """relu(obs @ w1^T + b1) for uint8 obs [B, 1800] and bf16 w1 [256, 1800], b1 [256] on the
+    GPU: one HIP MFMA kernel, fp32 accumulation, bf16 [B, 256] out."""
+    obs_u8 = obs_u8.contiguous()
+    w1, b1 = w1.contiguous(), b1.contiguous()
+    assert obs_u8.dtype == torch.uint8 and w1.dtype == b1.dtype == torch.bfloat16
+    assert w1.shape == (256, OBS) and b1.shape == (256,) and obs_u8.shape[1] == OBS
+    h = torch.empty((obs_u8.shape[0], 256), dtype=torch.bfloat16, device=obs_u8.device)
+    L = _lib.load()
+    _lib.check(L.d1_trunk1(obs_u8.data_ptr(), obs_u8.shape[0], w1.data_ptr(), b1.data_ptr(), h.data_ptr(),
+                           torch.cuda.current_stream(obs_u8.device).cuda_stream), 'd1_trunk1')
+    return h
 
 
 def widen(obs_u8, dtype):

@@ -153,6 +153,13 @@ int d1_sample_ar(const float *verb_logits, int nv, int ldv, const float *target_
                  uint64_t seed, uint32_t t, int32_t *verb, int32_t *target, int64_t *action, float *logp,
                  void *stream);
 
+/* The trunk's first layer as one MFMA kernel: h1 = relu(obs @ w1^T + b1) with obs
+ * uint8 [M, 1800] (8-byte aligned), w1 bf16 [256, 1800] (torch Linear layout, 16-byte
+ * aligned), b1 bf16 [256], fp32 accumulation, h1 bf16 [M, 256] (round to nearest even).
+ * Replaces the widening pass + library GEMM of the policy forward
+ * (gpu-d1/scripts/run_ring_ablations.py:209-223, BASELINE 1800->256 ReLU layer). */
+int d1_trunk1(const uint8_t *obs, int M, const void *w1, const void *b1, void *h1, void *stream);
+
 /* Widen `count` uint8 observation bytes to bf16 (exact), for the policy trunk.
  * count must be a multiple of 16 and both pointers 16-byte aligned. */
 int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stream);

@@ -19,7 +19,7 @@ def test_header_declares_the_abi():
                                          'd1_obs_to_bf16', 'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd',
                                          'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
                                          'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
-                                         'd1_sample_ar', 'd1_los_table'])
+                                         'd1_sample_ar', 'd1_los_table', 'd1_trunk1'])
     # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
     assert declared_symbols('d1learn.h', 'learn_') == sorted(
         ['learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size', 'learn_action_size',

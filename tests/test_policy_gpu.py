@@ -132,6 +132,23 @@ def reference_loss(logits, values, actions, old_logp, adv, ret, clip=0.2):
     return pg + .25 * (values - ret).square().mean() - 0.01 * dist.entropy().mean()
 
 
+@pytest.mark.parametrize('M', [1, 1000, 4096])
+def test_trunk1_matches_fp32_reference(M):
+    """The fused uint8 -> MFMA first layer vs relu(obs @ W1^T + b1) in fp32: within bf16
+    rounding of the output (2e-2 relative to the output scale), and vs torch's own bf16 GEMM."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    torch.manual_seed(M)
+    obs = torch.randint(0, 60, (M, 1800), dtype=torch.uint8, device='cuda')
+    w1 = (torch.randn(256, 1800, device='cuda') * 0.02).to(torch.bfloat16)
+    b1 = (torch.randn(256, device='cuda') * 0.1).to(torch.bfloat16)
+    h = P.trunk1(obs, w1, b1)
+    ref = torch.relu(obs.float() @ w1.float().T + b1.float())
+    scale = ref.abs().max().clamp_min(1e-3)
+    assert ((h.float() - ref).abs().max() / scale).item() < 2e-2
+    bf = torch.relu(torch.addmm(b1, obs.to(torch.bfloat16), w1.T))
+    assert ((h.float() - bf.float()).abs().max() / scale).item() < 2e-2
+
+
 def test_ppo_loss_matches_reference_fp32():
     ppo = importlib.import_module('dcss-auto_amd.ppo')
     g = torch.Generator().manual_seed(5)
