@@ -571,34 +571,68 @@ __device__ __forceinline__ void bfs_commit(Smem *sm, int y, Row nw, int layer) {
 // Bit-parallel BFS over floor from the player (the all-pairs row of
 // gpu-d1/scripts/learn_env.py:31-39), stopped `margin` layers after every mover is
 // reached. dist holds the layer mod 256; comparisons are relative (|delta| <= 25).
+// Lane l keeps rows l and (l < 6) 64+l of the frontier, reach and floor in registers;
+// vertical neighbours arrive by lane shuffles, so a layer needs no LDS round trip or
+// barrier. Reach is published to LDS at the end (the monster phase reads it), and the
+// frontier bitmap is cleared there for the repair search's queued-cell marks.
+__device__ __forceinline__ uint32_t lane_up(uint32_t v) { return (uint32_t)__shfl_up((int)v, 1); }
+__device__ __forceinline__ uint32_t lane_dn(uint32_t v) { return (uint32_t)__shfl_down((int)v, 1); }
+__device__ __forceinline__ Row row_up(Row r) { return {lane_up(r.a), lane_up(r.b), lane_up(r.c)}; }
+__device__ __forceinline__ Row row_dn(Row r) { return {lane_dn(r.a), lane_dn(r.b), lane_dn(r.c)}; }
+__device__ __forceinline__ Row row_lane(Row r, int l) {
+    return {(uint32_t)lane_val((int)r.a, l), (uint32_t)lane_val((int)r.b, l), (uint32_t)lane_val((int)r.c, l)};
+}
+__device__ __forceinline__ Row row_sel(bool c, Row x, Row y) { return c ? x : y; }
+__device__ __forceinline__ Row dilate(Row f, Row up, Row dn) {
+    Row v = row_or(f, row_or(up, dn));
+    return row_or(v, row_or(row_shl1(v), row_shr1(v)));
+}
 __device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
     Smem *sm = x.sm;
-    for (int w = x.lane; w < ROWS_WORDS; w += 64) { sm->reach[w] = 0; sm->front[w] = 0; }
-    __syncthreads();
-    if (x.lane == 0) {
-        int p = x.player;
-        sm->reach[(p / W) * RW + ((p % W) >> 5)] |= 1u << ((p % W) & 31);
-        sm->front[(p / W) * RW + ((p % W) >> 5)] |= 1u << ((p % W) & 31);
-        sm->dist[p] = 0;
-    }
-    __syncthreads();
+    const int lane = x.lane;
+    const bool has1 = lane < H - 64;
+    const Row zero{0, 0, 0};
+    const Row fl0 = row_ld(sm->floor, lane), fl1 = has1 ? row_ld(sm->floor, 64 + lane) : zero;
+    const int py = x.player / W, px = x.player % W;
+    const Row pbit = row_range(px, px);
+    Row f0 = lane == py ? pbit : zero, f1 = has1 && 64 + lane == py ? pbit : zero;
+    Row r0 = f0, r1 = f1;
+    if (lane == 0) sm->dist[x.player] = 0;
+    // this lane's monster cell: source lane and word of its row
+    const bool mover = (movers >> lane) & 1;
+    const int my = mover ? x.mpos / W : 0, mx = mover ? x.mpos % W : 0;
+    const int msrc = my & 63, mword = mx >> 5;
+    const uint32_t mbit = 1u << (mx & 31);
     int stop = 1 << 30;
-    const int y0 = x.lane, y1 = x.lane + 64;
     for (int layer = 1; layer < N; layer++) {
-        Row n0 = bfs_expand(sm, y0), n1 = y1 < H ? bfs_expand(sm, y1) : Row{0, 0, 0};
-        __syncthreads();
-        bfs_commit(sm, y0, n0, layer);
-        if (y1 < H) bfs_commit(sm, y1, n1, layer);
-        __syncthreads();
+        const Row f1_0 = row_lane(f1, 0), f0_63 = row_lane(f0, 63);
+        const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, f1_0, row_dn(f0));
+        const Row u1 = row_sel(lane == 0, f0_63, row_up(f1)), d1 = row_sel(lane >= H - 65, zero, row_dn(f1));
+        const Row n0 = row_andn(row_and(dilate(f0, u0, d0), fl0), r0);
+        const Row n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), fl1), r1) : zero;
+        r0 = row_or(r0, n0); r1 = row_or(r1, n1);
+        f0 = n0; f1 = n1;
+        scatter_layer(sm, lane * W, n0.a, layer);
+        scatter_layer(sm, lane * W + 32, n0.b, layer);
+        scatter_layer(sm, lane * W + 64, n0.c, layer);
+        if (has1) {
+            scatter_layer(sm, (64 + lane) * W, n1.a, layer);
+            scatter_layer(sm, (64 + lane) * W + 32, n1.b, layer);
+            scatter_layer(sm, (64 + lane) * W + 64, n1.c, layer);
+        }
         if (!ballot(row_any(n0) || row_any(n1))) break;
         if (stop == (1 << 30)) {
-            bool missing = ((movers >> x.lane) & 1) && !bit(sm->reach, x.mpos);
-            if (!ballot(missing)) stop = layer + margin;
+            const Row s0 = {(uint32_t)__shfl((int)r0.a, msrc), (uint32_t)__shfl((int)r0.b, msrc), (uint32_t)__shfl((int)r0.c, msrc)};
+            const Row s1 = {(uint32_t)__shfl((int)r1.a, msrc), (uint32_t)__shfl((int)r1.b, msrc), (uint32_t)__shfl((int)r1.c, msrc)};
+            const Row sr = my >= 64 ? s1 : s0;
+            const uint32_t w = mword == 0 ? sr.a : mword == 1 ? sr.b : sr.c;
+            if (!ballot(mover && !(w & mbit))) stop = layer + margin;
         }
         if (layer >= stop) break;
     }
-    __syncthreads();
-    for (int w = x.lane; w < ROWS_WORDS; w += 64) sm->front[w] = 0;   // the repair BFS's queued-cell marks
+    row_st(sm->reach, lane, r0);
+    row_st(sm->front, lane, zero);
+    if (has1) { row_st(sm->reach, 64 + lane, r1); row_st(sm->front, 64 + lane, zero); }
     __syncthreads();
 }
 // gpu-d1/src/sim.h:254-269
