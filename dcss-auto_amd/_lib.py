@@ -10,13 +10,26 @@ _LIB = None
 
 SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
            'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16',
-           'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd', 'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
-           'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
+           'd1_ppo_work_bytes', 'd1_ppo_step', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
            'd1_sample_ar', 'd1_los_table', 'd1_trunk1')
 LEARN_SYMBOLS = ('learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size',
                  'learn_action_size', 'learn_out_size', 'learn_config_bytes', 'learn_init', 'learn_step',
                  'learn_step_active', 'learn_heuristic')
 _LEARN = {}
+
+
+class D1PPOStep(C.Structure):
+    """The D1PPOStep struct of include/d1hip.h (one PPO minibatch update)."""
+    _fields_ = [('obs', C.c_void_p), ('perm', C.c_void_p), ('cursor', C.c_void_p), ('actions', C.c_void_p),
+                ('logp_old', C.c_void_p), ('adv', C.c_void_p), ('ret', C.c_void_p), ('n', C.c_int64),
+                ('mb', C.c_int32), ('pad0', C.c_int32), ('p', C.c_void_p), ('pb', C.c_void_p),
+                ('g', C.c_void_p), ('m', C.c_void_p), ('v', C.c_void_p), ('nparams', C.c_int64),
+                ('off_w1', C.c_int64), ('off_b1', C.c_int64), ('off_w2', C.c_int64), ('off_b2', C.c_int64),
+                ('off_w3', C.c_int64), ('off_b3', C.c_int64), ('w2t', C.c_void_p), ('w3t', C.c_void_p),
+                ('step', C.c_void_p), ('loss_parts', C.c_void_p), ('work', C.c_void_p),
+                ('work_bytes', C.c_int64), ('clip', C.c_float), ('vcoef', C.c_float), ('ecoef', C.c_float),
+                ('max_grad_norm', C.c_float), ('lr', C.c_float), ('beta1', C.c_float), ('beta2', C.c_float),
+                ('eps', C.c_float)]
 
 
 def load():
@@ -34,18 +47,13 @@ def load():
         L.d1_step.argtypes = [p, i, i, p, p, p, p, p, p, p, p]
         L.d1_sample.argtypes = [p, i, i, i, C.c_uint64, C.c_uint32, p, p, p]
         L.d1_obs_to_bf16.argtypes = [p, p, C.c_int64, p]
-        L.d1_ppo_gather.argtypes = [p, i, p, i, p, p, p, p, p, p, p, p, p, p]
-        L.d1_ppo_loss.argtypes = [p, i, i, p, p, p, p, i, C.c_float, C.c_float, C.c_float, p, p, p]
-        L.d1_relu_bwd.argtypes = [p, p, C.c_int64, p]
-        L.d1_relu_bwd_bias.argtypes = [p, p, i, i, p, i, p, p]
-        L.d1_colsum.argtypes = [p, i, i, i, p, i, p, p]
-        L.d1_sum_partials.argtypes = [p, i, C.c_int64, p, p]
+        L.d1_ppo_work_bytes.argtypes = [i]
+        L.d1_ppo_work_bytes.restype = C.c_int64
+        L.d1_ppo_step.argtypes = [C.POINTER(D1PPOStep), p]
         L.d1_sample_ar.argtypes = [p, i, i, p, i, i, i, C.c_uint64, C.c_uint32, p, p, p, p, p]
         L.d1_wait_bytes.argtypes = []
         L.d1_wait_init.argtypes = [p, i, i, p, p, C.c_uint64, i, p]
         L.d1_wait_run.argtypes = [p, i, i, p, p, i, p, p]
-        L.d1_adam_clip.argtypes = [p, p, p, p, p, C.c_int64, p, i, C.c_float, C.c_float, C.c_float, C.c_float,
-                                   C.c_float, p, p]
         L.d1_gae.argtypes = [p, p, p, p, i, i, C.c_float, C.c_float, p, p, p]
         L.d1_los_table.argtypes = [p, i, p, p, p]
         L.d1_trunk1.argtypes = [p, i, p, p, p, p]

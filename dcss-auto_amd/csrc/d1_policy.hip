@@ -143,243 +143,6 @@ __global__ __launch_bounds__(256) void k_u8_bf16(const uint4 *__restrict__ in, u
     out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
-// ---------------------------------------------------------------- PPO minibatch kernels
-// None of these clears memory with memset or reduces across workgroups through
-// atomics, so a captured graph of a minibatch step replays exactly.
-__device__ __forceinline__ float bf16_to_f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
-__device__ __forceinline__ uint16_t f_to_bf16(float f) {   // round to nearest even
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u) return (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
-// Row gather of a minibatch: obs rows -> bf16 (exact), plus the per-sample scalars.
-// One 128-lane workgroup per sample; `row_bytes` is a multiple of 8 (8 bytes in, 16 out per lane step).
-__global__ __launch_bounds__(128) void k_ppo_gather(const uint8_t *__restrict__ obs, int row_bytes,
-                                                    const int64_t *__restrict__ idx, const int64_t *__restrict__ act,
-                                                    const float *__restrict__ logp, const float *__restrict__ adv,
-                                                    const float *__restrict__ ret, uint16_t *__restrict__ xb,
-                                                    int32_t *__restrict__ act_o, float *__restrict__ logp_o,
-                                                    float *__restrict__ adv_o, float *__restrict__ ret_o) {
-    int i = blockIdx.x;
-    int64_t r = idx[i];
-    const uint2 *src = (const uint2 *)(obs + (size_t)r * row_bytes);
-    uint4 *dst = (uint4 *)(xb + (size_t)i * row_bytes);
-    for (int c = threadIdx.x; c < row_bytes / 8; c += blockDim.x) {
-        uint2 v = src[c];
-        uint32_t w[2] = {v.x, v.y}, o[4];
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            o[2 * j] = (__float_as_uint((float)(w[j] & 0xFFu)) >> 16) | (__float_as_uint((float)((w[j] >> 8) & 0xFFu)) & 0xFFFF0000u);
-            o[2 * j + 1] = (__float_as_uint((float)((w[j] >> 16) & 0xFFu)) >> 16) | (__float_as_uint((float)(w[j] >> 24)) & 0xFFFF0000u);
-        }
-        dst[c] = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-    if (threadIdx.x == 0) {
-        act_o[i] = (int32_t)act[r];
-        logp_o[i] = logp[r];
-        adv_o[i] = adv[r];
-        ret_o[i] = ret[r];
-    }
-}
-
-// Clipped-surrogate + value + entropy loss and its gradient w.r.t. the head output
-// z = [logits(k) | value] (bf16, row stride ldz). Per sample, with p = softmax(logits),
-// r = exp(logp_a - old):
-//   dL/dz_j = (g_r * r * ([j==a] - p_j) + ecoef * p_j * (log p_j + H)) / mb,
-//   g_r = -A when r*A <= clip(r)*A (torch.minimum routes ties to its first argument), else 0;
-//   dL/dvalue = vcoef * (v - R) / mb.
-// partial[b*4 + {0,1,2}] = this workgroup's sums of the per-sample pg, 0.5*(v-R)^2, H.
-__global__ __launch_bounds__(256) void k_ppo_loss(const uint16_t *__restrict__ z, int ldz, int k,
-                                                  const int32_t *__restrict__ act, const float *__restrict__ old_logp,
-                                                  const float *__restrict__ adv, const float *__restrict__ ret, int mb,
-                                                  float clip, float vcoef, float ecoef, uint16_t *__restrict__ dz,
-                                                  float *__restrict__ partial) {
-    __shared__ float red[3][256];
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    float pg = 0.f, vl = 0.f, ent = 0.f;
-    if (i < mb) {
-        constexpr int KMAX = 32;
-        const uint16_t *zi = z + (size_t)i * ldz;
-        float l[KMAX];
-        float m = -3.0e38f;
-#pragma unroll
-        for (int j = 0; j < KMAX; j++) { l[j] = j < k ? bf16_to_f(zi[j]) : -3.0e38f; m = fmaxf(m, l[j]); }
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < KMAX; j++) s += j < k ? expf(l[j] - m) : 0.f;
-        float ls = logf(s);
-        int a = act[i];
-        float h = 0.f, la = 0.f;
-#pragma unroll
-        for (int j = 0; j < KMAX; j++) {
-            if (j < k) { float lp = l[j] - m - ls; h -= expf(lp) * lp; }
-            if (j == a) la = l[j];
-        }
-        float lpa = la - m - ls;
-        float r = expf(lpa - old_logp[i]);
-        float A = adv[i];
-        float un = r * A, cl = fminf(fmaxf(r, 1.f - clip), 1.f + clip) * A;
-        pg = -fminf(un, cl);
-        float gr = un <= cl ? -A : 0.f;
-        float v = bf16_to_f(zi[k]), d = v - ret[i];
-        vl = 0.5f * d * d;
-        ent = h;
-        float inv = 1.f / (float)mb;
-        uint16_t *di = dz + (size_t)i * ldz;
-#pragma unroll
-        for (int j = 0; j < KMAX; j++) {
-            if (j < k) {
-                float lp = l[j] - m - ls, p = expf(lp);
-                float g = gr * r * ((j == a ? 1.f : 0.f) - p) + ecoef * p * (lp + h);
-                di[j] = f_to_bf16(g * inv);
-            }
-        }
-        di[k] = f_to_bf16(vcoef * d * inv);
-    }
-    red[0][threadIdx.x] = pg; red[1][threadIdx.x] = vl; red[2][threadIdx.x] = ent;
-    __syncthreads();
-    for (int o = blockDim.x / 2; o; o >>= 1) {
-        if ((int)threadIdx.x < o)
-            for (int q = 0; q < 3; q++) red[q][threadIdx.x] += red[q][threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x < 3) partial[blockIdx.x * 4 + threadIdx.x] = red[threadIdx.x][0];
-}
-
-// dh *= (h > 0), bf16, in place (ReLU backward).
-__global__ __launch_bounds__(256) void k_relu_bwd(uint16_t *__restrict__ dh, const uint16_t *__restrict__ h, size_t n) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n && !(bf16_to_f(h[i]) > 0.f)) dh[i] = 0;
-}
-
-// ReLU backward fused with the bias gradient: dh *= (h > 0) on a [rows, cols] bf16 block
-// (cols <= 256), and colpart[b*cols + c] = sum over this workgroup's rows of the masked dh.
-// Workgroup = 256 lanes, lane = column; rows split in chunks of `rows_per`.
-__global__ __launch_bounds__(256) void k_relu_bwd_bias(uint16_t *__restrict__ dh, const uint16_t *__restrict__ h,
-                                                       int rows, int cols, int rows_per, float *__restrict__ colpart) {
-    int c = threadIdx.x;
-    int r0 = blockIdx.x * rows_per, r1 = min(rows, r0 + rows_per);
-    float acc = 0.f;
-    if (c < cols) {
-        for (int r = r0; r < r1; r++) {
-            size_t o = (size_t)r * cols + c;
-            float v = bf16_to_f(dh[o]);
-            if (!(bf16_to_f(h[o]) > 0.f)) { v = 0.f; dh[o] = 0; }
-            acc += v;
-        }
-        colpart[(size_t)blockIdx.x * cols + c] = acc;
-    }
-}
-// Column sums of a [rows, cols] bf16 block into colpart (no masking).
-__global__ __launch_bounds__(256) void k_colsum(const uint16_t *__restrict__ x, int rows, int cols, int ld,
-                                                int rows_per, float *__restrict__ colpart) {
-    int c = threadIdx.x;
-    int r0 = blockIdx.x * rows_per, r1 = min(rows, r0 + rows_per);
-    if (c < cols) {
-        float acc = 0.f;
-        for (int r = r0; r < r1; r++) acc += bf16_to_f(x[(size_t)r * ld + c]);
-        colpart[(size_t)blockIdx.x * cols + c] = acc;
-    }
-}
-// out[c] = bf16(sum_b colpart[b*cols + c]); one workgroup per column, tree sum in LDS.
-__global__ __launch_bounds__(256) void k_colsum_finish(const float *__restrict__ colpart, int nblocks, int cols,
-                                                       uint16_t *__restrict__ out) {
-    __shared__ float red[256];
-    int c = blockIdx.x;
-    float acc = 0.f;
-    for (int b = threadIdx.x; b < nblocks; b += blockDim.x) acc += colpart[(size_t)b * cols + c];
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int o = blockDim.x / 2; o; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[c] = f_to_bf16(red[0]);
-}
-// out[j] = bf16(sum_s part[s*n + j]) over S split-K partials (bf16), 8 elements per lane.
-__global__ __launch_bounds__(256) void k_sum_partials(const uint16_t *__restrict__ part, int S, size_t n,
-                                                      uint16_t *__restrict__ out) {
-    size_t j = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-    if (j >= n) return;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (j + 8 <= n && (n % 8) == 0) {
-        for (int q = 0; q < S; q++) {
-            uint4 v = *(const uint4 *)(part + (size_t)q * n + j);
-            uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) { acc[2 * e] += bf16_to_f((uint16_t)w[e]); acc[2 * e + 1] += bf16_to_f((uint16_t)(w[e] >> 16)); }
-        }
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) o[e] = (uint32_t)f_to_bf16(acc[2 * e]) | ((uint32_t)f_to_bf16(acc[2 * e + 1]) << 16);
-        *(uint4 *)(out + j) = make_uint4(o[0], o[1], o[2], o[3]);
-    } else {
-        for (size_t k = j; k < n && k < j + 8; k++) {
-            float a = 0.f;
-            for (int q = 0; q < S; q++) a += bf16_to_f(part[(size_t)q * n + k]);
-            out[k] = f_to_bf16(a);
-        }
-    }
-}
-
-// Sum of squares of the bf16 gradient buffer: one partial per workgroup.
-__global__ __launch_bounds__(256) void k_sqnorm(const uint16_t *__restrict__ g, size_t n, float *__restrict__ partial,
-                                                float *__restrict__ step) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) step[1] = step[0] + 1.f;   // t for the Adam launch that follows
-    __shared__ float red[256];
-    float acc = 0.f;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        float v = bf16_to_f(g[i]);
-        acc += v * v;
-    }
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int o = blockDim.x / 2; o; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
-}
-
-// Gradient-norm clipping + Adam (torch.optim.Adam, no weight decay) over flat buffers.
-// Every workgroup re-sums the `nparts` norm partials (so no cross-workgroup handoff),
-// takes coef = min(max_norm / (||g|| + 1e-6), 1), and updates its slice. The step count:
-// k_sqnorm wrote t = step[0] + 1 to step[1]; every workgroup here reads step[1] and
-// workgroup 0 stores it back to step[0] for the next call.
-__global__ __launch_bounds__(256) void k_adam(float *__restrict__ p, uint16_t *__restrict__ pb,
-                                              const uint16_t *__restrict__ g, float *__restrict__ m,
-                                              float *__restrict__ v, size_t n, const float *__restrict__ partial,
-                                              int nparts, float max_norm, float lr, float b1, float b2, float eps,
-                                              float *__restrict__ step) {
-    __shared__ float red[256];
-    float acc = 0.f;
-    for (int j = threadIdx.x; j < nparts; j += blockDim.x) acc += partial[j];
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int o = blockDim.x / 2; o; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    float norm = sqrtf(red[0]);
-    float coef = fminf(max_norm / (norm + 1e-6f), 1.f);
-    float t = step[1];
-    float bc1 = 1.f - powf(b1, t), bc2 = 1.f - powf(b2, t);
-    float step_size = lr / bc1, bc2s = sqrtf(bc2);
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        float gi = bf16_to_f(g[i]) * coef;
-        float mi = b1 * m[i] + (1.f - b1) * gi;
-        float vi = b2 * v[i] + (1.f - b2) * gi * gi;
-        m[i] = mi;
-        v[i] = vi;
-        float pi = p[i] - step_size * mi / (sqrtf(vi) / bc2s + eps);
-        p[i] = pi;
-        pb[i] = f_to_bf16(pi);
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) step[0] = t;
-}
-
 }  // namespace d1p
 
 extern "C" {
@@ -409,71 +172,6 @@ int d1_obs_to_bf16(const uint8_t *obs, void *out, int64_t count, void *stream) {
     size_t n16 = (size_t)count / 16;
     hipLaunchKernelGGL(d1p::k_u8_bf16, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        (const uint4 *)obs, (uint4 *)out, n16);
-    return (int)hipGetLastError();
-}
-int d1_ppo_gather(const uint8_t *obs, int row_bytes, const int64_t *idx, int mb, const int64_t *act,
-                  const float *logp, const float *adv, const float *ret, void *xb, int32_t *act_o, float *logp_o,
-                  float *adv_o, float *ret_o, void *stream) {
-    if (mb < 0 || row_bytes <= 0 || (row_bytes % 8)) return D1_E_ARG;
-    if (mb && (!obs || !idx || !act || !logp || !adv || !ret || !xb || !act_o || !logp_o || !adv_o || !ret_o))
-        return D1_E_ARG;
-    if (mb == 0) return 0;
-    hipLaunchKernelGGL(d1p::k_ppo_gather, dim3(mb), dim3(128), 0, (hipStream_t)stream, obs, row_bytes, idx, act, logp,
-                       adv, ret, (uint16_t *)xb, act_o, logp_o, adv_o, ret_o);
-    return (int)hipGetLastError();
-}
-int d1_ppo_loss(const void *z, int ldz, int k, const int32_t *act, const float *old_logp, const float *adv,
-                const float *ret, int mb, float clip, float vcoef, float ecoef, void *dz, float *partial,
-                void *stream) {
-    if (mb < 0 || k < 1 || k > 32 || ldz < k + 1) return D1_E_ARG;
-    if (mb && (!z || !act || !old_logp || !adv || !ret || !dz || !partial)) return D1_E_ARG;
-    if (mb == 0) return 0;
-    hipLaunchKernelGGL(d1p::k_ppo_loss, dim3((mb + 255) / 256), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t *)z, ldz, k, act, old_logp, adv, ret, mb, clip, vcoef, ecoef, (uint16_t *)dz,
-                       partial);
-    return (int)hipGetLastError();
-}
-int d1_relu_bwd(void *dh, const void *h, int64_t n, void *stream) {
-    if (n < 0 || (n && (!dh || !h))) return D1_E_ARG;
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(d1p::k_relu_bwd, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       (uint16_t *)dh, (const uint16_t *)h, (size_t)n);
-    return (int)hipGetLastError();
-}
-int d1_relu_bwd_bias(void *dh, const void *h, int rows, int cols, float *colpart, int nblocks, void *bias_grad,
-                     void *stream) {
-    if (rows <= 0 || cols <= 0 || cols > 256 || nblocks < 1 || !dh || !h || !colpart || !bias_grad) return D1_E_ARG;
-    int per = (rows + nblocks - 1) / nblocks;
-    hipLaunchKernelGGL(d1p::k_relu_bwd_bias, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, (uint16_t *)dh,
-                       (const uint16_t *)h, rows, cols, per, colpart);
-    hipLaunchKernelGGL(d1p::k_colsum_finish, dim3(cols), dim3(256), 0, (hipStream_t)stream, colpart, nblocks, cols,
-                       (uint16_t *)bias_grad);
-    return (int)hipGetLastError();
-}
-int d1_colsum(const void *x, int rows, int cols, int ld, float *colpart, int nblocks, void *out, void *stream) {
-    if (rows <= 0 || cols <= 0 || cols > 256 || ld < cols || nblocks < 1 || !x || !colpart || !out) return D1_E_ARG;
-    int per = (rows + nblocks - 1) / nblocks;
-    hipLaunchKernelGGL(d1p::k_colsum, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, rows,
-                       cols, ld, per, colpart);
-    hipLaunchKernelGGL(d1p::k_colsum_finish, dim3(cols), dim3(256), 0, (hipStream_t)stream, colpart, nblocks, cols,
-                       (uint16_t *)out);
-    return (int)hipGetLastError();
-}
-int d1_sum_partials(const void *part, int S, int64_t n, void *out, void *stream) {
-    if (S < 1 || n <= 0 || !part || !out) return D1_E_ARG;
-    size_t threads = ((size_t)n + 7) / 8;
-    hipLaunchKernelGGL(d1p::k_sum_partials, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t *)part, S, (size_t)n, (uint16_t *)out);
-    return (int)hipGetLastError();
-}
-int d1_adam_clip(float *p, void *pb, const void *g, float *m, float *v, int64_t n, float *partial, int nparts,
-                 float max_norm, float lr, float b1, float b2, float eps, float *step, void *stream) {
-    if (n <= 0 || nparts < 1 || nparts > 4096 || !p || !pb || !g || !m || !v || !partial || !step)
-        return D1_E_ARG;
-    hipLaunchKernelGGL(d1p::k_sqnorm, dim3(nparts), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)g, (size_t)n,
-                       partial, step);
-    hipLaunchKernelGGL(d1p::k_adam, dim3(nparts), dim3(256), 0, (hipStream_t)stream, p, (uint16_t *)pb,
-                       (const uint16_t *)g, m, v, (size_t)n, partial, nparts, max_norm, lr, b1, b2, eps, step);
     return (int)hipGetLastError();
 }
 int d1_gae(const float *reward, const uint8_t *done, const float *value, const float *bootstrap, int T, int n,

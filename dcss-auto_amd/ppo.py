@@ -78,9 +78,9 @@ class PPO:
 
 
 # ----------------------------------------------------------------------------------------
-# Graph-safe PPO: explicit forward/backward over flat parameter buffers. Everything in the
-# minibatch step is a GEMM (hipBLASLt through torch) or a libd1hip kernel; no torch
-# reductions run inside the step, so the step can be captured in a HIP graph and replayed.
+# Graph-safe PPO: one libd1hip call (d1_ppo_step) per minibatch over flat parameter buffers.
+# The step picks its minibatch from a device-side cursor, so a HIP graph holding several
+# calls walks consecutive minibatches of the epoch's sample order.
 
 _PARAMS = (('l1.weight', (256, 1800)), ('l1.bias', (256,)), ('l2.weight', (256, 256)), ('l2.bias', (256,)),
            ('head.weight', (17, 256)), ('head.bias', (17,)))
@@ -119,108 +119,102 @@ class FlatParams:
 
 
 class FastPPO:
+    """PPO update with the minibatch step in libd1hip (four kernels: fused per-sample
+    forward/loss/backward, grouped split-K weight gradients, fixed-order reduction, clip +
+    Adam). Same interface and semantics as PPO with bf16 autocast; `minibatch` must be a
+    multiple of 1024. With graph=True, `graph_steps` consecutive minibatch steps are
+    captured in one HIP graph per buffer and replayed."""
+
     def __init__(self, policy, lr=3e-4, eps=1e-5, clip=0.2, vcoef=0.5, ecoef=0.01, max_grad_norm=0.5,
-                 epochs=4, minibatch=8192, gamma=0.99, lam=0.95, graph=True, nparts=512):
+                 epochs=4, minibatch=8192, gamma=0.99, lam=0.95, graph=True, graph_steps=16):
+        from . import _lib
+        if minibatch <= 0 or minibatch % 1024:
+            raise ValueError('FastPPO needs a minibatch that is a multiple of 1024')
         dev = next(policy.parameters()).device
-        self.flat = FlatParams(policy, dev)
+        self.flat = F = FlatParams(policy, dev)
         self.lr, self.eps, self.clip, self.vcoef, self.ecoef = lr, eps, clip, vcoef, ecoef
         self.max_grad_norm, self.epochs, self.minibatch, self.gamma, self.lam = max_grad_norm, epochs, minibatch, gamma, lam
-        self.graph, self.nparts, self.dev = graph, nparts, dev
-        mb = minibatch
+        self.graph, self.graph_steps, self.dev = graph, graph_steps, dev
         self.step_t = torch.zeros(2, dtype=torch.float32, device=dev)
-        self.norm_parts = torch.zeros(nparts, dtype=torch.float32, device=dev)
-        self.loss_parts = torch.zeros(((mb + 255) // 256) * 4, dtype=torch.float32, device=dev)
-        self.idx = torch.zeros(mb, dtype=torch.int64, device=dev)
-        self.xb = torch.empty((mb, OBS), dtype=torch.bfloat16, device=dev)
-        self.act = torch.empty(mb, dtype=torch.int32, device=dev)
-        self.old = torch.empty(mb, dtype=torch.float32, device=dev)
-        self.adv_mb = torch.empty(mb, dtype=torch.float32, device=dev)
-        self.ret_mb = torch.empty(mb, dtype=torch.float32, device=dev)
-        self.dz = torch.empty((mb, 17), dtype=torch.bfloat16, device=dev)
-        self.colblocks = 512
-        self.colpart = torch.zeros(self.colblocks * 256, dtype=torch.float32, device=dev)
-        self.splitk = 16 if mb % 16 == 0 else 1
-        self.kpart = torch.empty(self.splitk * 256 * OBS, dtype=torch.bfloat16, device=dev)
+        self.cursor = torch.zeros(2, dtype=torch.int32, device=dev)
+        self.loss_parts = torch.zeros(minibatch // 32 * 4, dtype=torch.float32, device=dev)
+        nbytes = _lib.load().d1_ppo_work_bytes(minibatch)
+        _lib.check(0 if nbytes > 0 else nbytes, 'd1_ppo_work_bytes')
+        self.work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        self.w2t = F.view(F.pb, 'l2.weight').t().contiguous()
+        self.w3t = torch.zeros((256, 32), dtype=torch.bfloat16, device=dev)
+        self.w3t[:, :17] = F.view(F.pb, 'head.weight').t()
+        self.perm = None
         self._g = self._g_buf = None
+        self._args = self._args_key = None
 
-    # one minibatch whose indices are in self.idx; buffers are flattened [T*N, ...] views
+    def _struct(self, obs, actions, logp, adv, ret):
+        from . import _lib
+        key = (obs.data_ptr(), actions.data_ptr(), logp.data_ptr(), adv.data_ptr(), ret.data_ptr(),
+               self.perm.data_ptr(), obs.shape[0])
+        if self._args_key != key:
+            F = self.flat
+            if obs.shape[1] != OBS or not obs.is_contiguous() or obs.dtype != torch.uint8:
+                raise ValueError('observations must be contiguous uint8 [n, 1800]')
+            off = {name: o for name, (o, _, _) in F.offsets.items()}
+            self._args = _lib.D1PPOStep(
+                obs=obs.data_ptr(), perm=self.perm.data_ptr(), cursor=self.cursor.data_ptr(),
+                actions=actions.data_ptr(), logp_old=logp.data_ptr(), adv=adv.data_ptr(), ret=ret.data_ptr(),
+                n=obs.shape[0], mb=self.minibatch, p=F.p.data_ptr(), pb=F.pb.data_ptr(), g=F.g.data_ptr(),
+                m=F.m.data_ptr(), v=F.v.data_ptr(), nparams=F.n, off_w1=off['l1.weight'], off_b1=off['l1.bias'],
+                off_w2=off['l2.weight'], off_b2=off['l2.bias'], off_w3=off['head.weight'],
+                off_b3=off['head.bias'], w2t=self.w2t.data_ptr(), w3t=self.w3t.data_ptr(),
+                step=self.step_t.data_ptr(), loss_parts=self.loss_parts.data_ptr(), work=self.work.data_ptr(),
+                work_bytes=self.work.numel(), clip=self.clip, vcoef=self.vcoef, ecoef=self.ecoef,
+                max_grad_norm=self.max_grad_norm, lr=self.lr, beta1=0.9, beta2=0.999, eps=self.eps)
+            self._args_key = key
+        return self._args
+
+    def set_order(self, perm):
+        """Sample order of the next minibatches (int64 [n] on the device); resets the cursor
+        so the next step takes perm[0:minibatch]."""
+        if self.perm is None or self.perm.shape != perm.shape:
+            self.perm = torch.empty_like(perm, dtype=torch.int64)
+        self.perm.copy_(perm)
+        self.cursor.zero_()
+
     def _step(self, obs, actions, logp, adv, ret):
+        """One minibatch: samples perm[cursor*mb : (cursor+1)*mb]; advances the cursor."""
         from . import _lib
-        L, F, s = _lib.load(), self.flat, torch.cuda.current_stream(self.dev).cuda_stream
-        mb = self.minibatch
-        _lib.check(L.d1_ppo_gather(obs.data_ptr(), obs.shape[1], self.idx.data_ptr(), mb, actions.data_ptr(),
-                                   logp.data_ptr(), adv.data_ptr(), ret.data_ptr(), self.xb.data_ptr(),
-                                   self.act.data_ptr(), self.old.data_ptr(), self.adv_mb.data_ptr(),
-                                   self.ret_mb.data_ptr(), s), 'd1_ppo_gather')
-        W1, b1 = F.view(F.pb, 'l1.weight'), F.view(F.pb, 'l1.bias')
-        W2, b2 = F.view(F.pb, 'l2.weight'), F.view(F.pb, 'l2.bias')
-        W3, b3 = F.view(F.pb, 'head.weight'), F.view(F.pb, 'head.bias')
-        h1 = torch._addmm_activation(b1, self.xb, W1.t())
-        h2 = torch._addmm_activation(b2, h1, W2.t())
-        z = torch.addmm(b3, h2, W3.t())
-        _lib.check(L.d1_ppo_loss(z.data_ptr(), 17, 16, self.act.data_ptr(), self.old.data_ptr(),
-                                 self.adv_mb.data_ptr(), self.ret_mb.data_ptr(), mb, self.clip, self.vcoef, self.ecoef,
-                                 self.dz.data_ptr(), self.loss_parts.data_ptr(), s), 'd1_ppo_loss')
-        G = lambda name: F.view(F.g, name)   # noqa: E731
-        cb, cp = self.colblocks, self.colpart.data_ptr()
-        self._wgrad(self.dz, h2, G('head.weight'))
-        _lib.check(L.d1_colsum(self.dz.data_ptr(), mb, 17, 17, cp, cb, G('head.bias').data_ptr(), s), 'd1_colsum')
-        dh2 = torch.mm(self.dz, W3)
-        _lib.check(L.d1_relu_bwd_bias(dh2.data_ptr(), h2.data_ptr(), mb, 256, cp, cb, G('l2.bias').data_ptr(), s),
-                   'd1_relu_bwd_bias')
-        self._wgrad(dh2, h1, G('l2.weight'))
-        dh1 = torch.mm(dh2, W2)
-        _lib.check(L.d1_relu_bwd_bias(dh1.data_ptr(), h1.data_ptr(), mb, 256, cp, cb, G('l1.bias').data_ptr(), s),
-                   'd1_relu_bwd_bias')
-        self._wgrad(dh1, self.xb, G('l1.weight'))
-        _lib.check(L.d1_adam_clip(F.p.data_ptr(), F.pb.data_ptr(), F.g.data_ptr(), F.m.data_ptr(), F.v.data_ptr(),
-                                  F.n, self.norm_parts.data_ptr(), self.nparts, self.max_grad_norm, self.lr, 0.9,
-                                  0.999, self.eps, self.step_t.data_ptr(), s), 'd1_adam_clip')
-
-    def _wgrad(self, dy, x, out):
-        """out = dy^T @ x with the batch (K) dimension split S ways: one bf16 bmm into
-        [S, M, N] partials (right operand contiguous), then a libd1hip partial sum."""
-        from . import _lib
-        S = self.splitk
-        if S == 1:
-            torch.mm(dy.t(), x, out=out)
-            return
-        mb, M = dy.shape
-        N = x.shape[1]
-        part = self.kpart[:S * M * N].view(S, M, N)
-        torch.bmm(dy.view(S, mb // S, M).transpose(1, 2), x.view(S, mb // S, N), out=part)
-        _lib.check(_lib.load().d1_sum_partials(part.data_ptr(), S, M * N, out.data_ptr(),
-                                               torch.cuda.current_stream(self.dev).cuda_stream), 'd1_sum_partials')
+        args = self._struct(obs, actions, logp, adv, ret)
+        _lib.check(_lib.load().d1_ppo_step(args, torch.cuda.current_stream(self.dev).cuda_stream), 'd1_ppo_step')
 
     def loss_terms(self):
         """(pg, value, entropy) means of the last minibatch (reads device partials)."""
-        parts = self.loss_parts.view(-1, 4)[:, :3].sum(0) / self.minibatch
-        return parts
+        return self.loss_parts.view(-1, 4)[:, :3].sum(0) / self.minibatch
 
     def _views(self, buf):
         n = buf.T * buf.N
         return buf.obs.view(n, -1), buf.actions.view(n), buf.logp.view(n)
 
+    def _graph_len(self, n):
+        steps = n // self.minibatch
+        k = max(1, min(self.graph_steps, steps))
+        while steps % k:
+            k -= 1
+        return k
+
     def _capture(self, buf):
         n = buf.T * buf.N
-        if n % self.minibatch:
-            raise ValueError('T*N must be a multiple of the minibatch size')
+        if n < self.minibatch:
+            raise ValueError('the buffer holds fewer samples than one minibatch')
         self._adv = torch.zeros(n, device=self.dev)
         self._ret = torch.zeros(n, device=self.dev)
+        if self.perm is None or self.perm.numel() != n:
+            self.perm = torch.zeros(n, dtype=torch.int64, device=self.dev)
         obs, actions, logp = self._views(buf)
-        saved = [t.clone() for t in (self.flat.p, self.flat.pb, self.flat.m, self.flat.v, self.step_t)]
-        side = torch.cuda.Stream(device=self.dev)
-        side.wait_stream(torch.cuda.current_stream(self.dev))
-        with torch.cuda.stream(side):
-            for _ in range(2):
-                self._step(obs, actions, logp, self._adv, self._ret)
-        torch.cuda.current_stream(self.dev).wait_stream(side)
+        args = self._struct(obs, actions, logp, self._adv, self._ret)
+        torch.cuda.synchronize(self.dev)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._step(obs, actions, logp, self._adv, self._ret)
-        for dst, src in zip((self.flat.p, self.flat.pb, self.flat.m, self.flat.v, self.step_t), saved):
-            dst.copy_(src)
-        self._g, self._g_buf = g, buf
+            for _ in range(self._graph_len(n)):
+                self._step(obs, actions, logp, self._adv, self._ret)
+        self._g, self._g_buf, self._g_args = g, buf, args
 
     def advantages(self, buf):
         adv, ret = P.gae(buf.rewards, buf.dones, buf.values, buf.bootstrap, self.gamma, self.lam)
@@ -235,15 +229,15 @@ class FastPPO:
                 self._capture(buf)
             self._adv.copy_(adv)
             self._ret.copy_(ret)
+            adv, ret = self._adv, self._ret
         obs, actions, logp = self._views(buf)
+        steps = n // self.minibatch            # a ragged tail is dropped (T*N is a multiple in C4)
         for _ in range(self.epochs):
-            perm = torch.randperm(n, device=self.dev, generator=generator)
-            for inds in perm.split(self.minibatch):
-                if len(inds) != self.minibatch:
-                    continue               # a ragged tail is dropped (T*N is a multiple in C4)
-                self.idx.copy_(inds)
-                if self.graph:
+            self.set_order(torch.randperm(n, device=self.dev, generator=generator))
+            if self.graph:
+                for _ in range(steps // self._graph_len(n)):
                     self._g.replay()
-                else:
+            else:
+                for _ in range(steps):
                     self._step(obs, actions, logp, adv, ret)
         return self.loss_terms()

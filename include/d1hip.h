@@ -164,35 +164,46 @@ int d1_trunk1(const uint8_t *obs, int M, const void *w1, const void *b1, void *h
  * count must be a multiple of 16 and both pointers 16-byte aligned. */
 int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stream);
 
-/* PPO minibatch pieces (graph-safe: no memsets, no cross-workgroup atomics).
- * d1_ppo_gather: rows idx[mb] of uint8 obs [*, row_bytes] -> bf16 xb [mb, row_bytes] and the
- *   per-sample action (int32), old log-prob, advantage and return.
- * d1_ppo_loss: clipped surrogate + vcoef*0.5*(v-R)^2 - ecoef*H on bf16 head outputs
- *   z [mb, ldz] = [k logits | value]; writes dL/dz (bf16, same layout) and per-workgroup
- *   partial sums (pg, value, entropy) to partial[4*ceil(mb/256)]
- *   (loss of gpu-d1/scripts/run_ring_ablations.py:364-367).
- * d1_relu_bwd: dh *= (h > 0) on bf16 buffers of n elements.
- * d1_adam_clip: global-norm clipping (max_norm) + Adam over flat fp32 params p (bf16 copy pb
- *   refreshed), bf16 grads g, fp32 moments m/v; partial holds nparts floats of scratch;
- *   step[0..1] is the device-side step counter (torch.optim.Adam semantics, no decay). */
-int d1_ppo_gather(const uint8_t *obs, int row_bytes, const int64_t *idx, int mb, const int64_t *act,
-                  const float *logp, const float *adv, const float *ret, void *xb, int32_t *act_o,
-                  float *logp_o, float *adv_o, float *ret_o, void *stream);
-int d1_ppo_loss(const void *z, int ldz, int k, const int32_t *act, const float *old_logp, const float *adv,
-                const float *ret, int mb, float clip, float vcoef, float ecoef, void *dz, float *partial,
-                void *stream);
-int d1_relu_bwd(void *dh, const void *h, int64_t n, void *stream);
-/* ReLU backward fused with the bias gradient of a [rows, cols<=256] bf16 block:
- * dh *= (h > 0) and bias_grad[c] = sum_r dh[r, c] (bf16), via nblocks partial rows in
- * colpart[nblocks*cols]; d1_colsum is the same column sum without the mask (row stride ld). */
-int d1_relu_bwd_bias(void *dh, const void *h, int rows, int cols, float *colpart, int nblocks, void *bias_grad,
-                     void *stream);
-int d1_colsum(const void *x, int rows, int cols, int ld, float *colpart, int nblocks, void *out, void *stream);
-/* out[j] = sum over s < S of part[s*n + j] (bf16 in, fp32 sum, bf16 out): the reduction
- * step of a split-K GEMM. */
-int d1_sum_partials(const void *part, int S, int64_t n, void *out, void *stream);
-int d1_adam_clip(float *p, void *pb, const void *g, float *m, float *v, int64_t n, float *partial, int nparts,
-                 float max_norm, float lr, float b1, float b2, float eps, float *step, void *stream);
+/* One PPO minibatch update of the 1800 -> 256 -> 256 ReLU policy with a 17-wide head
+ * (16 logits + value): gather through the sample order, forward, clipped-surrogate +
+ * value + entropy loss, backward, global-norm clipping and Adam on fp32 masters
+ * (gpu-d1/scripts/train_clear.py:160-172, gpu-d1/scripts/run_ring_ablations.py:363-372),
+ * computed as torch bf16 autocast does: bf16 operands, fp32 accumulation, bf16 results.
+ *
+ * Minibatch i = cursor[0] covers samples perm[i*mb .. i*mb+mb) of the rollout buffer; each
+ * call advances cursor[0] on the device, so a captured graph of several calls walks
+ * consecutive minibatches. A call whose minibatch would end past n changes nothing.
+ * Graph-safe: no memsets, no atomics; every reduction has a fixed order (bit-reproducible).
+ *
+ * Parameters live in flat buffers (element offsets off_* into p / pb / g / m / v, each a
+ * multiple of 8): l1.weight [256,1800], l1.bias [256], l2.weight [256,256], l2.bias [256],
+ * head.weight [17,256], head.bias [17] (torch Linear layouts). w2t (bf16 [256][256]) and w3t
+ * (bf16 [256][32], columns 17..31 zero) hold l2.weight^T and head.weight^T; the caller fills
+ * them once from pb and every call refreshes them with the updated weights. */
+typedef struct {
+    const uint8_t *obs;             /* [n, 1800] uint8 observations (8-byte aligned) */
+    const int64_t *perm;            /* [n] sample order, entries in [0, n) */
+    int32_t *cursor;                /* [2] device ints: cursor[0] = minibatch number, cursor[1] = scratch */
+    const int64_t *actions;         /* [n] */
+    const float *logp_old, *adv, *ret;   /* [n] */
+    int64_t n;                      /* samples in the buffer, < 2^31 */
+    int32_t mb;                     /* minibatch size, a multiple of 1024 */
+    int32_t pad0;
+    float *p;                       /* fp32 master parameters (16-byte aligned, like every flat buffer) */
+    void *pb;                       /* bf16 copy read by the forward */
+    void *g;                        /* bf16 gradients written by the call */
+    float *m, *v;                   /* Adam moments */
+    int64_t nparams;
+    int64_t off_w1, off_b1, off_w2, off_b2, off_w3, off_b3;
+    void *w2t, *w3t;
+    float *step;                    /* [2] Adam step count (torch.optim.Adam semantics, no decay) */
+    float *loss_parts;              /* [mb/32 * 4]: per 32 samples the sums of pg, 0.5*(v-R)^2, entropy */
+    void *work;                     /* d1_ppo_work_bytes(mb) bytes of device scratch, 256-byte aligned */
+    int64_t work_bytes;
+    float clip, vcoef, ecoef, max_grad_norm, lr, beta1, beta2, eps;
+} D1PPOStep;
+int64_t d1_ppo_work_bytes(int mb);
+int d1_ppo_step(const D1PPOStep *s, void *stream);
 
 /* Reverse-time GAE over a [T, n] rollout (gpu-d1/scripts/run_ring_ablations.py:354-360):
  *   live = 1 - done[t]; delta = reward[t] + (gamma*next)*live - value[t];

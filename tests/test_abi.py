@@ -16,9 +16,8 @@ def declared_symbols(header='d1hip.h', prefix='d1_'):
 def test_header_declares_the_abi():
     assert declared_symbols() == sorted(['d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size',
                                          'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_gae',
-                                         'd1_obs_to_bf16', 'd1_ppo_gather', 'd1_ppo_loss', 'd1_relu_bwd',
-                                         'd1_adam_clip', 'd1_relu_bwd_bias', 'd1_colsum',
-                                         'd1_sum_partials', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
+                                         'd1_obs_to_bf16', 'd1_ppo_work_bytes', 'd1_ppo_step',
+                                         'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
                                          'd1_sample_ar', 'd1_los_table', 'd1_trunk1'])
     # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
     assert declared_symbols('d1learn.h', 'learn_') == sorted(
@@ -78,3 +77,39 @@ def test_argument_validation_without_gpu(pkg):
     shared = pkg.reference_config()
     assert L.d1_init(1, 4, 40, C.byref(shared), C.byref(tab), 0, None, None, None) == -1  # shared map missing
     assert L.d1_step(1, 0, 8, C.byref(cfg), C.byref(tab), 1, None, None, None, None, None) == 0  # empty batch
+
+
+def test_ppo_step_struct_layout(tmp_path):
+    """The ctypes D1PPOStep and the C struct agree field by field (gcc on the header)."""
+    import importlib
+    import subprocess
+    _lib = importlib.import_module('dcss-auto_amd._lib')
+    names = [f for f, _ in _lib.D1PPOStep._fields_]
+    src = tmp_path / 'layout.c'
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "d1hip.h"\nint main(void) {\n'
+                   '  printf("%zu\\n", sizeof(D1PPOStep));\n' +
+                   ''.join(f'  printf("%zu\\n", offsetof(D1PPOStep, {f}));\n' for f in names) + '  return 0;\n}\n')
+    exe = tmp_path / 'layout'
+    subprocess.run(['gcc', '-I', str(ROOT / 'include'), '-o', str(exe), str(src)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert got[0] == C.sizeof(_lib.D1PPOStep)
+    assert got[1:] == [getattr(_lib.D1PPOStep, f).offset for f in names]
+
+
+def test_ppo_step_validation_without_gpu(pkg):
+    """Workspace sizing and rejected PPO arguments need no GPU."""
+    import importlib
+    _lib = importlib.import_module('dcss-auto_amd._lib')
+    L = _lib.load()
+    assert L.d1_ppo_work_bytes(1000) == -1 and L.d1_ppo_work_bytes(0) == -1
+    w8k = L.d1_ppo_work_bytes(8192)
+    # 4 activation/gradient arrays [256][mb] + dz [17][mb] (bf16), bias partials, split-K partials
+    assert w8k >= 4 * 256 * 8192 * 2 + 8 * 256 * 1800 * 4
+    assert L.d1_ppo_work_bytes(4096) < w8k
+    assert L.d1_ppo_step(None, None) == -1
+    s = _lib.D1PPOStep(mb=1000, n=4096)
+    assert L.d1_ppo_step(C.byref(s), None) == -1                  # minibatch not a multiple of 1024
+    s = _lib.D1PPOStep(mb=1024, n=512)
+    assert L.d1_ppo_step(C.byref(s), None) == -1                  # fewer samples than one minibatch
+    s = _lib.D1PPOStep(mb=1024, n=4096)
+    assert L.d1_ppo_step(C.byref(s), None) == -1                  # null buffers

@@ -202,23 +202,27 @@ def _small_buffer(T, N, seed=3):
 
 
 def test_fast_ppo_gradients_match_autograd():
-    """Explicit backward (libd1hip loss/ReLU kernels + GEMMs) vs torch autograd under bf16
-    autocast on the same minibatch: gradients within the bf16 bar (2e-2 relative to the
-    gradient scale), loss terms within 1e-5 of the fp32 formula on the same head outputs."""
+    """The fused minibatch step (libd1hip d1_ppo_step) vs torch autograd under bf16 autocast
+    on the same minibatch, taken through a shuffled order: gradients within the bf16 bar
+    (2e-2 relative to the gradient scale), loss terms within 2e-2; the Adam step from zero
+    moments (no clipping) moves every weight by lr * g / (|g| + eps), checked to 1e-6."""
     P = importlib.import_module('dcss-auto_amd.policy')
     ppo = importlib.import_module('dcss-auto_amd.ppo')
-    T, N, mb = 2, 4096, 8192
+    T, N, mb = 4, 4096, 8192
     buf = _small_buffer(T, N)
     model = P.Policy(seed=4).cuda()
     fast = ppo.FastPPO(model, minibatch=mb, graph=False, max_grad_norm=1e9)
+    p0 = fast.flat.p.clone()
     adv, ret = fast.advantages(buf)
     obs, actions, logp = fast._views(buf)
-    fast.idx.copy_(torch.arange(mb, device='cuda'))
+    perm = torch.randperm(T * N, device='cuda', generator=torch.Generator(device='cuda').manual_seed(1))
+    fast.set_order(perm)
     fast._step(obs, actions, logp, adv, ret)
-    x = obs[:mb]
+    assert fast.cursor[0].item() == 1
+    inds = perm[:mb]
     with torch.autocast('cuda', dtype=torch.bfloat16):
-        logits, value = model(x)
-    loss, pg, vl, ent = ppo.ppo_loss(logits, value, actions[:mb], logp[:mb], adv[:mb], ret[:mb])
+        logits, value = model(obs[inds])
+    loss, pg, vl, ent = ppo.ppo_loss(logits, value, actions[inds], logp[inds], adv[inds], ret[inds])
     loss.backward()
     terms = fast.loss_terms()
     torch.testing.assert_close(terms, torch.stack([pg, vl, ent]).float(), rtol=2e-2, atol=1e-4)
@@ -227,29 +231,69 @@ def test_fast_ppo_gradients_match_autograd():
         scale = prm.grad.abs().max().item() + 1e-12
         err = (g - prm.grad).abs().max().item() / scale
         assert err < 2e-2, (name, err)
+    g = fast.flat.g.float()
+    want = p0 - fast.lr * g / (g.abs() + fast.eps)
+    torch.testing.assert_close(fast.flat.p, want, rtol=0, atol=1e-6)
+    for name in ('l2.weight', 'head.weight'):   # the transposed copies the next step reads
+        w = fast.flat.view(fast.flat.pb, name)
+        got = fast.w2t if name == 'l2.weight' else fast.w3t[:, :17]
+        assert torch.equal(got, w.t())
+    assert not fast.w3t[:, 17:].any()
 
 
 def test_fast_ppo_graph_replays_match_eager():
-    """Captured vs eager minibatch steps, with eager torch reductions between replays: the
-    flat parameters must agree bit for bit after every replay."""
+    """A graph of two minibatch steps vs eager steps over two epochs, with eager torch
+    reductions between replays: parameters, step count and cursor agree bit for bit after
+    every replay; a replay past the end of the order changes nothing."""
     P = importlib.import_module('dcss-auto_amd.policy')
     ppo = importlib.import_module('dcss-auto_amd.ppo')
     T, N, mb = 4, 4096, 4096
+    n = T * N
     buf = _small_buffer(T, N)
     eager = ppo.FastPPO(P.Policy(seed=2).cuda(), minibatch=mb, graph=False)
-    graphed = ppo.FastPPO(P.Policy(seed=2).cuda(), minibatch=mb, graph=True)
+    graphed = ppo.FastPPO(P.Policy(seed=2).cuda(), minibatch=mb, graph=True, graph_steps=2)
     graphed._capture(buf)
     adv, ret = eager.advantages(buf)
     graphed._adv.copy_(adv)
     graphed._ret.copy_(ret)
     obs, actions, logp = eager._views(buf)
-    for r in range(8):
-        inds = torch.randperm(T * N, device='cuda')[:mb]
-        eager.idx.copy_(inds)
-        eager._step(obs, actions, logp, adv, ret)
-        graphed.idx.copy_(inds)
-        graphed._g.replay()
-        torch.cuda.synchronize()
-        _ = torch.randn(1000, device='cuda').sum().item()      # eager reductions between replays
-        assert torch.equal(eager.flat.p, graphed.flat.p), f'replay {r}'
-        assert torch.equal(eager.step_t, graphed.step_t)
+    for epoch in range(2):
+        perm = torch.randperm(n, device='cuda')
+        eager.set_order(perm)
+        graphed.set_order(perm)
+        for r in range(2):
+            eager._step(obs, actions, logp, adv, ret)
+            eager._step(obs, actions, logp, adv, ret)
+            graphed._g.replay()
+            torch.cuda.synchronize()
+            _ = torch.randn(1000, device='cuda').sum().item()      # eager reductions between replays
+            assert torch.equal(eager.flat.p, graphed.flat.p), f'epoch {epoch} replay {r}'
+            assert torch.equal(eager.step_t, graphed.step_t)
+            assert torch.equal(eager.cursor[:1], graphed.cursor[:1])
+    assert graphed.cursor[0].item() == n // mb
+    before = graphed.flat.p.clone()
+    graphed._g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(graphed.flat.p, before) and graphed.cursor[0].item() == n // mb
+
+
+def test_fast_ppo_update_tracks_autograd_ppo():
+    """A whole update (GAE, 2 epochs x 4 minibatches, same shuffles) through FastPPO and
+    through the autograd PPO: every parameter moves the same way (cosine of the two
+    parameter deltas > 0.9) and the loss terms stay finite."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    ppo = importlib.import_module('dcss-auto_amd.ppo')
+    T, N, mb = 4, 4096, 4096
+    buf = _small_buffer(T, N, seed=7)
+    ref_model = P.Policy(seed=6).cuda()
+    p0 = {k: v.detach().clone() for k, v in ref_model.named_parameters()}
+    fast = ppo.FastPPO(P.Policy(seed=6).cuda(), minibatch=mb, epochs=2)
+    ref = ppo.PPO(ref_model, minibatch=mb, epochs=2)
+    fast_terms = fast.update(buf, generator=torch.Generator(device='cuda').manual_seed(11))
+    ref.update(buf, generator=torch.Generator(device='cuda').manual_seed(11))
+    for name, prm in ref_model.named_parameters():
+        d_ref = (prm.detach() - p0[name]).flatten()
+        d_fast = (fast.flat.view(fast.flat.p, name) - p0[name]).flatten()
+        cos = torch.nn.functional.cosine_similarity(d_ref, d_fast, dim=0).item()
+        assert cos > 0.9, (name, cos)
+    assert torch.isfinite(fast_terms).all()
