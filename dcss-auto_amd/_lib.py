@@ -10,7 +10,7 @@ _LIB = None
 
 SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
            'd1_init', 'd1_step', 'd1_sample', 'd1_gae', 'd1_obs_to_bf16',
-           'd1_ppo_work_bytes', 'd1_ppo_step', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
+           'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
            'd1_sample_ar', 'd1_los_table', 'd1_trunk1')
 LEARN_SYMBOLS = ('learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size',
                  'learn_action_size', 'learn_out_size', 'learn_config_bytes', 'learn_init', 'learn_step',
@@ -25,8 +25,7 @@ class D1PPOStep(C.Structure):
                 ('mb', C.c_int32), ('pad0', C.c_int32), ('p', C.c_void_p), ('pb', C.c_void_p),
                 ('g', C.c_void_p), ('m', C.c_void_p), ('v', C.c_void_p), ('nparams', C.c_int64),
                 ('off_w1', C.c_int64), ('off_b1', C.c_int64), ('off_w2', C.c_int64), ('off_b2', C.c_int64),
-                ('off_w3', C.c_int64), ('off_b3', C.c_int64), ('w2t', C.c_void_p), ('w3t', C.c_void_p),
-                ('step', C.c_void_p), ('loss_parts', C.c_void_p), ('work', C.c_void_p),
+                ('off_w3', C.c_int64), ('off_b3', C.c_int64), ('step', C.c_void_p), ('loss_parts', C.c_void_p), ('work', C.c_void_p),
                 ('work_bytes', C.c_int64), ('clip', C.c_float), ('vcoef', C.c_float), ('ecoef', C.c_float),
                 ('max_grad_norm', C.c_float), ('lr', C.c_float), ('beta1', C.c_float), ('beta2', C.c_float),
                 ('eps', C.c_float)]
@@ -50,6 +49,7 @@ def load():
         L.d1_ppo_work_bytes.argtypes = [i]
         L.d1_ppo_work_bytes.restype = C.c_int64
         L.d1_ppo_step.argtypes = [C.POINTER(D1PPOStep), p]
+        L.d1_ppo_prepare.argtypes = [C.POINTER(D1PPOStep), p]
         L.d1_sample_ar.argtypes = [p, i, i, p, i, i, i, C.c_uint64, C.c_uint32, p, p, p, p, p]
         L.d1_wait_bytes.argtypes = []
         L.d1_wait_init.argtypes = [p, i, i, p, p, C.c_uint64, i, p]

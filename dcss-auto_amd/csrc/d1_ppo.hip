@@ -10,20 +10,26 @@
 //             z = h2 W3^T + b3, the loss and dL/dz, dh2 = (dz W3)[h2 > 0] and
 //             dh1 = (dh2 W2)[h1 > 0], with per-workgroup bias-gradient and loss partials.
 //             Wave w owns columns 32w..32w+31 of every layer; activations cross waves through
-//             LDS, and leave for the weight gradients as [feature][sample] bf16 arrays.
+//             LDS, and leave for the weight gradients in fragment order (below).
 //   k_wgrad   dW1 = dh1^T x, dW2 = dh2^T h1, dW3 = dz^T h2 in one grouped launch of split-K
-//             MFMA tiles with fp32 partials. x is re-read through the sample order and
-//             transposed to [feature][sample] through LDS.
+//             MFMA tiles with fp32 partials.
 //   k_reduce  fixed-order sums of the partials -> bf16 gradients (one rounding, as the bf16
 //             GEMM gives), and sum-of-squares partials for the clipping norm.
-//   k_adam    global-norm clip + Adam on the fp32 masters, the bf16 copy, the transposed
-//             W2 / W3 copies the next k_rows reads, and the minibatch cursor.
+//   k_adam    global-norm clip + Adam on the fp32 masters, the bf16 copy, the fragment-ordered
+//             weight copies the next k_rows reads, and the minibatch cursor.
 //
 // MFMA: v_mfma_f32_32x32x16_bf16. Lane layouts (checked on the hardware): A lane l holds
 // A[l%32][8(l/32)+j], B lane l holds B[8(l/32)+j][l%32], D lane l holds
 // D[8(r/4)+4(l/32)+r%4][l%32]. The contraction order inside a 64-wide K chunk is free as
-// long as A and B agree, so in chunk k0, step q, slot j of a lane in half h stands for
-// k = k0 + 32h + 8q + j: each lane then reads 32 contiguous K values per operand row.
+// long as A and B agree, so in chunk c, step q, slot j of a lane in half h stands for
+// k = 64c + 32h + 8q + j.
+//
+// Fragment order. An operand that the MFMAs read as [row][k] (32-row block b, K chunk c,
+// step q) is stored so that the 64 lanes' 16-byte pieces of one step are one contiguous
+// kilobyte: element (row, k) at ((((b * nchunks + c) * 4 + q) * 64 + row%32 + 32h) * 8 + j).
+// Every operand load is then one fully used 1 KB span instead of 32 rows x 32 bytes. The
+// weights are kept in this order by k_adam (and d1_ppo_prepare), the activations and
+// gradients by k_rows; the uint8 x copy uses 16-byte pieces (two per lane and chunk).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -40,21 +46,32 @@ constexpr int NA = 16, NZ = 17;       // logits, head width
 constexpr int R = 32;                 // samples per k_rows workgroup
 constexpr int XS = H + 8;             // LDS row stride (bf16) of the [32][256] activation tiles
 constexpr int DS = 40;                // LDS row stride (bf16) of the dz tile (32 columns used)
+constexpr int XR = K1 + 16;           // LDS row stride (bf16) of k_rows' x tile: 908 dwords, so the
+                                      // 16-byte fragment reads of 16 consecutive rows hit distinct banks
 constexpr int BP = 544;               // bias partial row: db1[256] | db2[256] | db3[17] | pad
-constexpr int KW = 1024;              // samples per dW1 / dW2 workgroup
-constexpr int KW3 = 512;              // samples per dW3 workgroup
-constexpr int NT1 = (K1 + 63) / 64;   // dW1 column tiles of 64 (the last one holds 8 columns)
-constexpr int XR = K1 + 8;            // LDS row stride (bytes) of k_rows' x tile
-constexpr int NRED = 512;             // k_reduce weight workgroups (+ NBIAS for the biases)
-constexpr int NBIASB = (2 * H + NZ + 63) / 64;   // k_reduce bias workgroups (64 columns each)
-constexpr int NADAM = 1024;           // k_adam workgroups
+constexpr int C1 = 29;                // layer-1 K chunks (28 of 64 + the 8 inputs 1792..1799)
+constexpr int XB = 57;                // 32-row blocks of the x copy (1824 rows, 1800..1823 zero)
+constexpr int KW = 1024;              // samples per dW1 workgroup
+constexpr int KW2 = 512;              // samples per dW2 / dW3 workgroup
+constexpr int NT1 = 29;               // dW1 column tiles of 64 (the last one holds 8 columns)
+constexpr int NRED = (H * K1 + H * H + NZ * H) / 4 / 256 + 1;   // k_reduce weight workgroups: one unit per lane
+constexpr int NBIASB = (2 * H + NZ + 7) / 8;     // k_reduce bias workgroups (8 columns x 32 lanes each)
+
+// packed weight copies (bf16 elements), all in fragment order
+constexpr int P_W1 = 0;                          // layer 1 B (W1 rows): [8 blocks][29 chunks][4][64][8]
+constexpr int P_W2 = P_W1 + 8 * C1 * 4 * 512;    // layer 2 B (W2 rows): [8][4][4][64][8]
+constexpr int P_W2T = P_W2 + 8 * 4 * 4 * 512;    // dh1 B (W2 columns): [8][4][4][64][8]
+constexpr int P_W3 = P_W2T + 8 * 4 * 4 * 512;    // head B (W3 rows, 17 of 32 lanes): [8][2][64][8]
+constexpr int P_W3T = P_W3 + 8 * 2 * 512;        // dh2 B (W3 columns, k < 17): [8][2][64][8]
+constexpr int P_END = P_W3T + 8 * 2 * 512;
 
 struct Work {
-    uint16_t *h1t, *h2t, *dh2t, *dh1t;   // [256][mb] bf16
-    uint16_t *dzt;                       // [17][mb] bf16
-    uint8_t *xt;                         // [1800][mb] the minibatch's observations, transposed
+    uint16_t *wpk;                       // packed weights (state kept between calls)
+    uint16_t *h1f, *h2f, *dh2f, *dh1f;   // [256 rows][mb] bf16, fragment order
+    uint16_t *dzf;                       // [32 rows (17 used)][mb] bf16, fragment order
+    uint8_t *xf;                         // [1824 rows][mb] uint8 x^T, 16-byte fragment order
     float *bpart;                        // [mb/32][BP]
-    float *part1, *part2, *part3;        // [S1][256][1800], [S1][256][256], [S3][17][256]
+    float *part1, *part2, *part3;        // [mb/KW][256][1800], [mb/KW2][256][256], [mb/KW2][17][256]
     float *npart;                        // [NRED + NBIASB] sum-of-squares partials
 };
 
@@ -71,6 +88,12 @@ __device__ __forceinline__ uint32_t widen2(uint32_t x, int s) {
     uint32_t hi = __float_as_uint((float)((x >> (8 * s + 8)) & 255u)) & 0xFFFF0000u;
     return lo | hi;
 }
+// four bytes -> four bf16 (exact): the high halves of the converted floats, paired by v_perm
+__device__ __forceinline__ uint2 widen4(uint32_t x) {
+    const uint32_t f0 = __float_as_uint((float)(x & 255u)), f1 = __float_as_uint((float)((x >> 8) & 255u));
+    const uint32_t f2 = __float_as_uint((float)((x >> 16) & 255u)), f3 = __float_as_uint((float)(x >> 24));
+    return make_uint2(__builtin_amdgcn_perm(f1, f0, 0x07060302u), __builtin_amdgcn_perm(f3, f2, 0x07060302u));
+}
 __device__ __forceinline__ bf16x8 widen8(uint32_t x0, uint32_t x1) {
     return __builtin_bit_cast(bf16x8, make_uint4(widen2(x0, 0), widen2(x0, 2), widen2(x1, 0), widen2(x1, 2)));
 }
@@ -85,13 +108,37 @@ __device__ __forceinline__ bool cursor_ok(const D1PPOStep &a) {
 }
 // D row of accumulator register r in lane half h
 __device__ __forceinline__ int drow(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+// fragment-order index of element (row, k) of a [rows][nch*64] bf16 operand
+__device__ __forceinline__ size_t fidx(int row, int k, int nch) {
+    return ((((size_t)(row >> 5) * nch + (k >> 6)) * 4 + ((k >> 3) & 3)) * 64 + (row & 31) + 32 * ((k >> 5) & 1)) * 8 +
+           (k & 7);
+}
+// the same for the uint8 x copy: 16-byte pieces, two per lane and chunk
+__device__ __forceinline__ size_t xidx(int row, int k, int nch) {
+    return ((((size_t)(row >> 5) * nch + (k >> 6)) * 2 + ((k >> 4) & 1)) * 64 + (row & 31) + 32 * ((k >> 5) & 1)) * 16 +
+           (k & 15);
+}
+// packed-weight slots of each parameter element
+__device__ __forceinline__ int pk_w1(int n, int k) { return P_W1 + (int)fidx(n, k, C1); }     // W1[n][k]
+__device__ __forceinline__ int pk_w2(int n, int k) { return P_W2 + (int)fidx(n, k, 4); }      // W2[n][k]
+__device__ __forceinline__ int pk_w2t(int o, int i) { return P_W2T + (int)fidx(i, o, 4); }    // W2[o][i] as B[o][i]
+__device__ __forceinline__ int pk_w3(int j, int k) {   // head: wave k/32 contracts k = 32w + 16s + 8h + jj
+    return P_W3 + (((k >> 5) * 2 + ((k >> 4) & 1)) * 64 + j + 32 * ((k >> 3) & 1)) * 8 + (k & 7);
+}
+__device__ __forceinline__ int pk_w3t(int j, int c) {  // dh2: slot 8h + jj of step s is k = j = 16s + 8h + jj
+    return P_W3T + (((c >> 5) * 2 + (j >> 4)) * 64 + (c & 31) + 32 * ((j >> 3) & 1)) * 8 + (j & 7);
+}
+// one fragment (16 bytes per lane) of a packed operand
+__device__ __forceinline__ bf16x8 frag(const uint16_t *base, int idx, int lane) {
+    return as_bf(*(const uint4 *)(base + ((size_t)idx * 64 + lane) * 8));
+}
 
 // ---------------------------------------------------------------- k_rows
 // Epilogue shared by the four row-block products: v[r] (fp32, this lane's column c) ->
-// bf16 bits, LDS row-major tile (if any), the [c][sample] global array, bit r of *mask set
-// where the bf16 value is > 0 (if asked), and the column sum of the bf16 values (lanes < 32
-// hold the full 32-row sum afterwards).
-__device__ __forceinline__ float rows_out(const float (&v)[16], uint16_t *tile, uint16_t *gt, int mb, int m0, int c,
+// bf16 bits, LDS row-major tile (if any), the fragment-ordered global copy (rows = columns
+// c, k = samples), bit r of *mask set where the bf16 value is > 0 (if asked), and the column
+// sum of the bf16 values (lanes < 32 hold the full 32-row sum afterwards).
+__device__ __forceinline__ float rows_out(const float (&v)[16], uint16_t *tile, uint16_t *gf, int nch, int m0, int c,
                                           int lh, uint32_t *mask) {
     uint16_t hb[16];
     float colsum = 0.f;
@@ -105,132 +152,153 @@ __device__ __forceinline__ float rows_out(const float (&v)[16], uint16_t *tile, 
     }
     if (mask) *mask = pos;
 #pragma unroll
-    for (int g = 0; g < 4; g++)   // rows 8g + 4h .. +3 are registers 4g .. 4g+3
-        *(uint2 *)(gt + (size_t)c * mb + m0 + 8 * g + 4 * lh) =
+    for (int g = 0; g < 4; g++)   // samples m0 + 8g + 4h .. +3 are registers 4g .. 4g+3
+        *(uint2 *)(gf + fidx(c, m0 + 8 * g + 4 * lh, nch)) =
             make_uint2((uint32_t)hb[4 * g] | ((uint32_t)hb[4 * g + 1] << 16),
                        (uint32_t)hb[4 * g + 2] | ((uint32_t)hb[4 * g + 3] << 16));
     return colsum + __shfl_xor(colsum, 32);
 }
 
 __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
-    // The 32 x rows (layer 1) share their LDS with the tiles of the later phases.
-    __shared__ __align__(16) uint8_t lds[R * XR];
-    uint8_t *xs = lds;                                                       // x rows, stride XR
+    // The 32 x rows, widened once to bf16 (116 KB of the CU's 160 KB), share their LDS with
+    // the tiles of the later phases.
+    __shared__ __align__(16) uint8_t lds[R * XR * 2];
+    uint16_t *xs = (uint16_t *)lds;                                          // x rows (bf16), stride XR
     uint16_t *x1 = (uint16_t *)lds;                                          // h1, later dh2 (row-major)
     uint16_t *x2 = (uint16_t *)(lds + R * XS * 2);                           // h2
     uint16_t *dzs = (uint16_t *)(lds + 2 * R * XS * 2);                      // dL/dz, columns 17..31 zero
     float(*zp)[R][NZ] = (float(*)[R][NZ])(lds + 2 * R * XS * 2 + R * DS * 2);   // head partials per wave
-    static_assert(2 * R * XS * 2 + R * DS * 2 + 8 * R * NZ * 4 <= R * XR, "LDS union");
-    __shared__ int64_t srow[R];
+    static_assert(2 * R * XS * 2 + R * DS * 2 + 8 * R * NZ * 4 <= R * XR * 2, "LDS union");
+    __shared__ int64_t soff[R];   // byte offset of each sample's observation row
     __shared__ float sold[R], sadv[R], sret[R];
     __shared__ int sact[R];
+    __shared__ float lsum[8][3];
+    __shared__ float dzsum[8][NZ];
     if (!cursor_ok(a)) return;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lr = lane & 31, lh = lane >> 5;
-    const int mb = a.mb, m0 = blockIdx.x * R;
+    const int mb = a.mb, nch = mb / 64, m0 = blockIdx.x * R;
     const int64_t base = (int64_t)a.cursor[0] * mb + m0;
     const uint16_t *pb = (const uint16_t *)a.pb;
-    const uint16_t *W1 = pb + a.off_w1, *B1 = pb + a.off_b1, *W2 = pb + a.off_w2, *B2 = pb + a.off_b2;
-    const uint16_t *W3 = pb + a.off_w3, *B3 = pb + a.off_b3;
-    const uint16_t *W2T = (const uint16_t *)a.w2t, *W3T = (const uint16_t *)a.w3t;
+    const uint16_t *B1 = pb + a.off_b1, *B2 = pb + a.off_b2, *B3 = pb + a.off_b3;
+    const uint16_t *wpk = w.wpk;
+    const int c = 32 * wave + lr;   // this lane's column in every layer
+
+    // layer-1 weights: 4-deep ring of fragment-ordered chunks, the first three issued now
+    uint4 wb[4][4];
+    auto wload = [&](uint4 (&dst)[4], int ch) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) dst[q] = *(const uint4 *)(wpk + P_W1 + ((size_t)((wave * C1 + ch) * 4 + q) * 64 + lane) * 8);
+    };
+    wload(wb[0], 0);
+    wload(wb[1], 1);
+    wload(wb[2], 2);
     if (t < R) {
         const int64_t s = clamp_index(a.perm[base + t], a.n);   // entries outside [0, n) are a caller error
-        srow[t] = s;
+        soff[t] = s * K1;
         sact[t] = (int)a.actions[s];
         sold[t] = a.logp_old[s];
         sadv[t] = a.adv[s];
         sret[t] = a.ret[s];
     }
     __syncthreads();
-    {   // the 32 observation rows -> LDS: every load in flight at once
-        constexpr int XU = K1 / 8, NU = (R * XU + 511) / 512;
-        uint2 tmp[NU];
+    // The 32 observation rows, in units of 16 rows x 4 inputs: widened to bf16 into the LDS
+    // tile, and transposed in registers into the x^T copy for the dW1 product, one 16-byte
+    // piece per input (rows 1800..1823 of the copy are written as zeros). Inputs 0..895
+    // (chunks 0..13) are stored first; the loads of the rest are in flight meanwhile and are
+    // stored once layer 1 reaches chunk 14, so the gather overlaps the weight stream.
+    constexpr int KA = 224, KBN = K1 / 4 - KA;   // 4-input groups of each half
+    uint32_t xa[16], xb[16];
+    const int ua = min(t, 2 * KA - 1), pa = ua / KA, ka = ua - pa * KA;
+    const int ub = min(t, 2 * KBN - 1), pbb = ub / KBN, kb = KA + ub - pbb * KBN;
 #pragma unroll
-        for (int i = 0; i < NU; i++) {
-            const int u = t + 512 * i, r = u / XU, cc = u - r * XU;
-            tmp[i] = u < R * XU ? *(const uint2 *)(a.obs + srow[r] * K1 + 8 * cc) : make_uint2(0u, 0u);
+    for (int j = 0; j < 16; j++) xa[j] = *(const uint32_t *)(a.obs + soff[16 * pa + j] + 4 * ka);   // unconditional:
+#pragma unroll
+    for (int j = 0; j < 16; j++) xb[j] = *(const uint32_t *)(a.obs + soff[16 * pbb + j] + 4 * kb);  // spare lanes repeat
+    auto xstore = [&](const uint32_t (&x)[16], int p, int kg) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) *(uint2 *)(xs + (16 * p + j) * XR + 4 * kg) = widen4(x[j]);
+        // 4x4 byte transposes with v_perm: o[e][d] = byte e of samples 4d..4d+3
+        uint32_t o[4][4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t *y = &x[4 * d];
+            const uint32_t a01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);   // y0.0 y1.0 y0.1 y1.1
+            const uint32_t b01 = __builtin_amdgcn_perm(y[1], y[0], 0x07030602u);   // y0.2 y1.2 y0.3 y1.3
+            const uint32_t a23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+            const uint32_t b23 = __builtin_amdgcn_perm(y[3], y[2], 0x07030602u);
+            o[0][d] = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+            o[1][d] = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+            o[2][d] = __builtin_amdgcn_perm(b23, b01, 0x05040100u);
+            o[3][d] = __builtin_amdgcn_perm(b23, b01, 0x07060302u);
         }
-#pragma unroll
-        for (int i = 0; i < NU; i++) {
-            const int u = t + 512 * i, r = u / XU, cc = u - r * XU;
-            if (u < R * XU) *(uint2 *)(xs + r * XR + 8 * cc) = tmp[i];
-        }
-    }
-    __syncthreads();
-    // x^T for the dW1 product: xt[k][m0 + r], 4 inputs x 4 samples per unit, transposed in registers
-    for (int u = t; u < (K1 / 4) * (R / 4); u += 512) {
-        const int rg = u & 7, kg = u >> 3;
-        uint32_t x[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) x[i] = *(const uint32_t *)(xs + (4 * rg + i) * XR + 4 * kg);
 #pragma unroll
         for (int e = 0; e < 4; e++)
-            *(uint32_t *)(w.xt + (size_t)(4 * kg + e) * mb + m0 + 4 * rg) =
-                ((x[0] >> (8 * e)) & 255u) | (((x[1] >> (8 * e)) & 255u) << 8) | (((x[2] >> (8 * e)) & 255u) << 16) |
-                (((x[3] >> (8 * e)) & 255u) << 24);
-    }
-    const int c = 32 * wave + lr;   // this lane's column in every layer
+            *(uint4 *)(w.xf + xidx(4 * kg + e, m0 + 16 * p, nch)) = make_uint4(o[e][0], o[e][1], o[e][2], o[e][3]);
+    };
+    if (t < 2 * KA) xstore(xa, pa, ka);
+    if (t < 2 * (XB * 32 - K1))
+        *(uint4 *)(w.xf + xidx(K1 + (t >> 1), m0 + 16 * (t & 1), nch)) = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
     float v[16];
 
-    // ---- layer 1: 28 chunks of 64 inputs (A from the LDS rows, W1 through a 4-deep register
-    // ring, loads issued 3 chunks ahead), then k = 1792..1799 (lower half, q = 0)
+    // ---- layer 1: 28 chunks of 64 inputs (A from the LDS rows, W1 from the ring, loads
+    // issued 3 chunks ahead), then chunk 28 = inputs 1792..1799 (lower half, q = 0)
     uint32_t mask1 = 0, mask2 = 0;
+    bf16x8 w2f[16];   // layer-2 weight fragments (chunk ch, step q at 4 ch + q), then dh1's
     {
-        const uint8_t *xr = xs + lr * XR + 32 * lh;
-        const uint16_t *wr = W1 + (size_t)c * K1 + 32 * lh;
+        const uint16_t *xr = xs + lr * XR + 32 * lh;
         floatx16 e0 = {}, e1 = {};
-        uint4 wb[4][4];
-        auto wload = [&](uint4 (&dst)[4], int ch) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) dst[q] = *(const uint4 *)(wr + 64 * ch + 8 * q);
-        };
-        wload(wb[0], 0);
-        wload(wb[1], 1);
-        wload(wb[2], 2);
-        for (int ch0 = 0; ch0 < 28; ch0 += 4) {
+        for (int i0 = 0; i0 < 28; i0 += 4) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const int ch = ch0 + u;
-                if (ch + 3 < 28) wload(wb[(u + 3) & 3], ch + 3);
-                const uint4 lo = *(const uint4 *)(xr + 64 * ch), hi = *(const uint4 *)(xr + 64 * ch + 16);
-                e0 = mfma(widen8(lo.x, lo.y), as_bf(wb[u][0]), e0);
-                e1 = mfma(widen8(lo.z, lo.w), as_bf(wb[u][1]), e1);
-                e0 = mfma(widen8(hi.x, hi.y), as_bf(wb[u][2]), e0);
-                e1 = mfma(widen8(hi.z, hi.w), as_bf(wb[u][3]), e1);
+                const int ch = i0 + u;
+                if (ch == 14) {   // the second half of the x rows (uniform branch)
+                    if (t < 2 * KBN) xstore(xb, pbb, kb);
+                    __syncthreads();
+                }
+                if (ch + 3 < C1) wload(wb[(u + 3) & 3], ch + 3);
+                e0 = mfma(as_bf(*(const uint4 *)(xr + 64 * ch)), as_bf(wb[u][0]), e0);
+                e1 = mfma(as_bf(*(const uint4 *)(xr + 64 * ch + 8)), as_bf(wb[u][1]), e1);
+                e0 = mfma(as_bf(*(const uint4 *)(xr + 64 * ch + 16)), as_bf(wb[u][2]), e0);
+                e1 = mfma(as_bf(*(const uint4 *)(xr + 64 * ch + 24)), as_bf(wb[u][3]), e1);
             }
         }
-        const uint2 xt = lh == 0 ? *(const uint2 *)(xs + lr * XR + 1792) : make_uint2(0u, 0u);
-        const uint4 wt = lh == 0 ? *(const uint4 *)(W1 + (size_t)c * K1 + 1792) : make_uint4(0u, 0u, 0u, 0u);
-        e0 = mfma(widen8(xt.x, xt.y), as_bf(wt), e0);
+        // chunk 28 sits in ring slot 0 (loaded during chunk 25); its slots past input 1799 hold zeros
+        const uint4 xt = lh == 0 ? *(const uint4 *)(xs + lr * XR + 1792) : make_uint4(0u, 0u, 0u, 0u);
+        e0 = mfma(as_bf(xt), as_bf(wb[0][0]), e0);
+#pragma unroll
+        for (int q = 0; q < 16; q++) w2f[q] = frag(wpk + P_W2, wave * 16 + q, lane);   // layer 2's weights
         __syncthreads();   // every wave is done with the x rows before h1 overwrites them
         const float bias = bf(B1[c]);
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = fmaxf(e0[r] + e1[r] + bias, 0.f);
-        rows_out(v, x1, w.h1t, mb, m0, c, lh, &mask1);
+        rows_out(v, x1, w.h1f, nch, m0, c, lh, &mask1);
     }
     __syncthreads();
 
     // ---- layer 2: h2 = relu(h1 W2^T + b2), K = 256 from the LDS h1 tile
     {
         const uint16_t *ar = x1 + lr * XS + 32 * lh;
-        const uint16_t *br = W2 + (size_t)c * H + 32 * lh;
         floatx16 e0 = {}, e1 = {};
 #pragma unroll
-        for (int k0 = 0; k0 < H; k0 += 64) {
+        for (int ch = 0; ch < 4; ch++) {
             bf16x8 fa[4], fb[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                fa[q] = as_bf(*(const uint4 *)(ar + k0 + 8 * q));
-                fb[q] = as_bf(*(const uint4 *)(br + k0 + 8 * q));
+                fa[q] = as_bf(*(const uint4 *)(ar + 64 * ch + 8 * q));
+                fb[q] = w2f[4 * ch + q];
             }
             e0 = mfma(fa[0], fb[0], e0);
             e1 = mfma(fa[1], fb[1], e1);
             e0 = mfma(fa[2], fb[2], e0);
             e1 = mfma(fa[3], fb[3], e1);
         }
+#pragma unroll
+        for (int q = 0; q < 16; q++) w2f[q] = frag(wpk + P_W2T, wave * 16 + q, lane);   // dh1's weights
         const float bias = bf(B2[c]);
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = fmaxf(e0[r] + e1[r] + bias, 0.f);
-        rows_out(v, x2, w.h2t, mb, m0, c, lh, &mask2);
+        rows_out(v, x2, w.h2f, nch, m0, c, lh, &mask2);
     }
     __syncthreads();
 
@@ -239,10 +307,8 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         floatx16 zacc = {};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const int k = 32 * wave + 16 * s + 8 * lh;
-            const uint4 av = *(const uint4 *)(x2 + lr * XS + k);
-            const uint4 bv = lr < NZ ? *(const uint4 *)(W3 + (size_t)lr * H + k) : make_uint4(0u, 0u, 0u, 0u);
-            zacc = mfma(as_bf(av), as_bf(bv), zacc);
+            const uint4 av = *(const uint4 *)(x2 + lr * XS + 32 * wave + 16 * s + 8 * lh);
+            zacc = mfma(as_bf(av), frag(wpk + P_W3, wave * 2 + s, lane), zacc);
         }
         if (lr < NZ) {
 #pragma unroll
@@ -251,115 +317,103 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
     }
     __syncthreads();
 
-    // ---- loss and dL/dz: wave 0, lane = sample (k_ppo formula, k = 16 logits)
-    if (wave == 0) {
-        float pg = 0.f, vl = 0.f, ent = 0.f;
-        if (lane < R) {
-            const int r = lane;
-            float l[NZ];
+    // ---- loss and dL/dz: 16 lanes per sample (lane j = logit j; lane 0 also the value)
+    {
+        const int r = t >> 4, j = t & 15;
+        float zj = zp[0][r][j], zv = zp[0][r][NA];
 #pragma unroll
-            for (int j = 0; j < NZ; j++) {
-                float s = zp[0][r][j];
+        for (int q = 1; q < 8; q++) zj += zp[q][r][j], zv += zp[q][r][NA];
+        const float l = bf(rb(zj + bf(B3[j])));         // the head output is bf16
+        const float value = bf(rb(zv + bf(B3[NA])));
+        float mx = l;
 #pragma unroll
-                for (int q = 1; q < 8; q++) s += zp[q][r][j];
-                l[j] = bf(rb(s + bf(B3[j])));   // the head output is bf16
-            }
-            float mx = l[0];
+        for (int o = 8; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+        float se = expf(l - mx);
 #pragma unroll
-            for (int j = 1; j < NA; j++) mx = fmaxf(mx, l[j]);
-            float se = 0.f;
+        for (int o = 8; o; o >>= 1) se += __shfl_xor(se, o, 16);
+        const float ls = logf(se);
+        const float lp = l - mx - ls, p = expf(lp);
+        const int act = sact[r];
+        float hh = -p * lp, la = j == act ? l : 0.f;
 #pragma unroll
-            for (int j = 0; j < NA; j++) se += expf(l[j] - mx);
-            const float ls = logf(se);
-            const int act = sact[r];
-            float hh = 0.f, la = 0.f;
-#pragma unroll
-            for (int j = 0; j < NA; j++) {
-                const float lp = l[j] - mx - ls;
-                hh -= expf(lp) * lp;
-                if (j == act) la = l[j];
-            }
-            const float lpa = la - mx - ls;
-            const float ratio = expf(lpa - sold[r]);
-            const float A = sadv[r];
-            const float un = ratio * A, cl = fminf(fmaxf(ratio, 1.f - a.clip), 1.f + a.clip) * A;
-            pg = -fminf(un, cl);
-            const float gr = un <= cl ? -A : 0.f;   // torch.minimum routes ties to its first argument
-            const float d = l[NA] - sret[r];
-            vl = 0.5f * d * d;
-            ent = hh;
-            const float inv = 1.f / (float)mb;
-            uint16_t dz[32];
-#pragma unroll
-            for (int j = 0; j < NA; j++) {
-                const float lp = l[j] - mx - ls, p = expf(lp);
-                const float gj = gr * ratio * ((j == act ? 1.f : 0.f) - p) + a.ecoef * p * (lp + hh);
-                dz[j] = rb(gj * inv);
-            }
-            dz[NA] = rb(a.vcoef * d * inv);
-#pragma unroll
-            for (int j = NZ; j < 32; j++) dz[j] = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                uint4 u;
-                u.x = (uint32_t)dz[8 * q] | ((uint32_t)dz[8 * q + 1] << 16);
-                u.y = (uint32_t)dz[8 * q + 2] | ((uint32_t)dz[8 * q + 3] << 16);
-                u.z = (uint32_t)dz[8 * q + 4] | ((uint32_t)dz[8 * q + 5] << 16);
-                u.w = (uint32_t)dz[8 * q + 6] | ((uint32_t)dz[8 * q + 7] << 16);
-                *(uint4 *)(dzs + r * DS + 8 * q) = u;
-            }
-#pragma unroll
-            for (int j = 0; j < NZ; j++) w.dzt[(size_t)j * mb + m0 + r] = dz[j];
+        for (int o = 8; o; o >>= 1) {
+            hh += __shfl_xor(hh, o, 16);
+            la += __shfl_xor(la, o, 16);
         }
+        const float lpa = la - mx - ls;
+        const float ratio = expf(lpa - sold[r]);
+        const float A = sadv[r];
+        const float un = ratio * A, cl = fminf(fmaxf(ratio, 1.f - a.clip), 1.f + a.clip) * A;
+        const float gr = un <= cl ? -A : 0.f;   // torch.minimum routes ties to its first argument
+        const float d = value - sret[r];
+        const float inv = 1.f / (float)mb;
+        const uint16_t dzj = rb((gr * ratio * ((j == act ? 1.f : 0.f) - p) + a.ecoef * p * (lp + hh)) * inv);
+        dzs[r * DS + j] = dzj;
+        dzs[r * DS + NZ + j] = 0;   // columns 17..32 (32 is padding)
+        w.dzf[fidx(j, m0 + r, nch)] = dzj;
+        if (j == 0) {
+            const uint16_t dzv = rb(a.vcoef * d * inv);
+            dzs[r * DS + NA] = dzv;
+            w.dzf[fidx(NA, m0 + r, nch)] = dzv;
+        }
+        // column sums of dz over this wave's 4 samples (lanes j, j+16, j+32, j+48)
+        float cj = bf(dzj), cv = j == 0 ? bf(rb(a.vcoef * d * inv)) : 0.f;
 #pragma unroll
-        for (int o = 32; o; o >>= 1) {
+        for (int o = 32; o >= 16; o >>= 1) {
+            cj += __shfl_xor(cj, o);
+            cv += __shfl_xor(cv, o);
+        }
+        if (lane < 16) dzsum[wave][j] = cj;
+        if (lane == 0) dzsum[wave][NA] = cv;
+        // per-sample loss terms (every lane of a group holds them): lane j == 0 of each group
+        float pg = j == 0 ? -fminf(un, cl) : 0.f, vl = j == 0 ? 0.5f * d * d : 0.f, ent = j == 0 ? hh : 0.f;
+#pragma unroll
+        for (int o = 32; o >= 16; o >>= 1) {
             pg += __shfl_xor(pg, o);
             vl += __shfl_xor(vl, o);
             ent += __shfl_xor(ent, o);
         }
-        if (lane == 0) {
-            float *lp = a.loss_parts + (size_t)blockIdx.x * 4;
-            lp[0] = pg;
-            lp[1] = vl;
-            lp[2] = ent;
-            lp[3] = 0.f;
-        }
+        if (lane == 0) lsum[wave][0] = pg, lsum[wave][1] = vl, lsum[wave][2] = ent;
     }
     __syncthreads();
-    if (t < NZ) {   // head-bias partial
+    if (t < 4) {
         float s = 0.f;
-        for (int r = 0; r < R; r++) s += bf(dzs[r * DS + t]);
-        w.bpart[(size_t)blockIdx.x * BP + 2 * H + t] = s;
+        if (t < 3)
+            for (int q = 0; q < 8; q++) s += lsum[q][t];
+        a.loss_parts[(size_t)blockIdx.x * 4 + t] = s;
+    } else if (t >= 64 && t < 64 + NZ) {   // head-bias partial: the 8 waves' sums
+        float s = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) s += dzsum[q][t - 64];
+        w.bpart[(size_t)blockIdx.x * BP + 2 * H + (t - 64)] = s;
     }
 
-    // ---- dh2 = (dz W3)[h2 > 0]: K = 17 padded to 32, B = W3^T rows
+    // ---- dh2 = (dz W3)[h2 > 0]: K = 17 padded to 32, B = W3 columns
     {
         floatx16 acc = {};
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const uint4 av = *(const uint4 *)(dzs + lr * DS + 16 * s + 8 * lh);
-            const uint4 bv = *(const uint4 *)(W3T + (size_t)c * 32 + 16 * s + 8 * lh);
-            acc = mfma(as_bf(av), as_bf(bv), acc);
+            acc = mfma(as_bf(av), frag(wpk + P_W3T, wave * 2 + s, lane), acc);
         }
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = (mask2 >> r) & 1u ? acc[r] : 0.f;
-        const float cs = rows_out(v, x1, w.dh2t, mb, m0, c, lh, nullptr);
+        const float cs = rows_out(v, x1, w.dh2f, nch, m0, c, lh, nullptr);
         if (lh == 0) w.bpart[(size_t)blockIdx.x * BP + H + c] = cs;
     }
     __syncthreads();
 
-    // ---- dh1 = (dh2 W2)[h1 > 0]: K = 256 from the LDS dh2 tile, B = W2^T rows
+    // ---- dh1 = (dh2 W2)[h1 > 0]: K = 256 from the LDS dh2 tile, B = W2 columns
     {
         const uint16_t *ar = x1 + lr * XS + 32 * lh;
-        const uint16_t *br = W2T + (size_t)c * H + 32 * lh;
         floatx16 e0 = {}, e1 = {};
 #pragma unroll
-        for (int k0 = 0; k0 < H; k0 += 64) {
+        for (int ch = 0; ch < 4; ch++) {
             bf16x8 fa[4], fb[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                fa[q] = as_bf(*(const uint4 *)(ar + k0 + 8 * q));
-                fb[q] = as_bf(*(const uint4 *)(br + k0 + 8 * q));
+                fa[q] = as_bf(*(const uint4 *)(ar + 64 * ch + 8 * q));
+                fb[q] = w2f[4 * ch + q];
             }
             e0 = mfma(fa[0], fb[0], e0);
             e1 = mfma(fa[1], fb[1], e1);
@@ -368,94 +422,96 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         }
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = (mask1 >> r) & 1u ? e0[r] + e1[r] : 0.f;
-        const float cs = rows_out(v, nullptr, w.dh1t, mb, m0, c, lh, nullptr);
+        const float cs = rows_out(v, nullptr, w.dh1f, nch, m0, c, lh, nullptr);
         if (lh == 0) w.bpart[(size_t)blockIdx.x * BP + c] = cs;
     }
 }
 
 // ---------------------------------------------------------------- k_wgrad
-// One split-K tile of out[i][j] = sum_m at[i][m] bt[j][m] over samples [ms, ms + ks): both
-// operands are [row][sample] (K-contiguous); `at` bf16, `bt` bf16 or (XB) uint8. Wave w owns
-// NA_ row blocks of 32 from i0, the workgroup's NB_ column blocks of 32 from j0; rows past
-// arows / brows read as zero. Loads run through a RING-deep register ring (issued RING-1
-// chunks of 64 samples ahead); ks / 64 is a multiple of RING.
-template <int NA_, int NB_, bool XB, int RING>
-__device__ __forceinline__ void wgrad_tile(const uint16_t *at, int arows, int i0, const void *bt, int brows, int j0,
-                                           int mb, int ms, int ks, floatx16 (&acc)[NA_][NB_]) {
-    constexpr int BW = XB ? 2 : 4;   // uint4 per B row and chunk
-    const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
-    const uint16_t *ar[NA_];
-    bool aok[NA_];
+// One split-K tile of out[i][j] = sum_m at[i][m] bt[j][m] over the sample chunks
+// [c0, c0 + nc): both operands fragment-ordered with `nch` chunks; `at` bf16, `bt` bf16 or
+// (XB_) the uint8 x copy. Wave w owns NA_ row blocks of 32 from row block ib, the workgroup
+// NB_ column blocks from jb; row blocks at or past an / bn, and rows >= arows_last within
+// the last A block, read as zero. Loads run through a RING-deep register ring (issued
+// RING-1 chunks ahead); the walk over the chunks starts at chunk c0 + rot and wraps, so
+// that tiles reading the same operand rows at the same time read different chunks.
+template <int NA_, int NB_, bool XB_, int RING>
+__device__ __forceinline__ void wgrad_tile(const uint16_t *at, int ib, int an, int arows_last, const void *bt, int jb,
+                                           int bn, int nch, int c0, int nc, int rot, floatx16 (&acc)[NA_][NB_]) {
+    constexpr int BW = XB_ ? 2 : 4;   // 16-byte pieces per B row block and chunk
+    const int lane = threadIdx.x & 63, lr = lane & 31;
+    bool aok[NA_], bok[NB_];
 #pragma unroll
-    for (int i = 0; i < NA_; i++) {
-        aok[i] = i0 + 32 * i + lr < arows;
-        ar[i] = at + (size_t)(aok[i] ? i0 + 32 * i + lr : 0) * mb + ms + 32 * lh;
-    }
-    const uint4 *br[NB_];
-    bool bok[NB_];
+    for (int i = 0; i < NA_; i++) aok[i] = ib + i < an && (ib + i < an - 1 || lr < arows_last);
 #pragma unroll
-    for (int b = 0; b < NB_; b++) {
-        bok[b] = j0 + 32 * b + lr < brows;
-        const size_t row = bok[b] ? j0 + 32 * b + lr : 0;
-        br[b] = XB ? (const uint4 *)((const uint8_t *)bt + row * mb + ms + 32 * lh)
-                   : (const uint4 *)((const uint16_t *)bt + row * mb + ms + 32 * lh);
-    }
+    for (int b = 0; b < NB_; b++) bok[b] = jb + b < bn;
     uint4 av[RING][NA_][4], bv[RING][NB_][BW];
     auto load = [&](int slot, int ch) {
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
             for (int i = 0; i < NA_; i++)
-                av[slot][i][q] = aok[i] ? *(const uint4 *)(ar[i] + 64 * ch + 8 * q) : make_uint4(0u, 0u, 0u, 0u);
+                av[slot][i][q] = aok[i] ? *(const uint4 *)(at + ((((size_t)(ib + i) * nch + ch) * 4 + q) * 64 + lane) * 8)
+                                        : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-        for (int q = 0; q < BW; q++)
-#pragma unroll
-            for (int b = 0; b < NB_; b++)
-                bv[slot][b][q] = bok[b] ? br[b][(XB ? 4 : 8) * ch + q] : make_uint4(0u, 0u, 0u, 0u);
-    };
-    const int nch = ks / 64;
-#pragma unroll
-    for (int u = 0; u + 1 < RING; u++) load(u, u);
-    for (int ch0 = 0; ch0 < nch; ch0 += RING) {
-#pragma unroll
-        for (int u = 0; u < RING; u++) {
-            const int ch = ch0 + u;
-            if (ch + RING - 1 < nch) load((u + RING - 1) % RING, ch + RING - 1);
-            bf16x8 fb[NB_][4];
+        for (int p = 0; p < BW; p++)
 #pragma unroll
             for (int b = 0; b < NB_; b++) {
-                if (XB) {
-                    fb[b][0] = widen8(bv[u][b][0].x, bv[u][b][0].y);
-                    fb[b][1] = widen8(bv[u][b][0].z, bv[u][b][0].w);
-                    fb[b][2] = widen8(bv[u][b][1].x, bv[u][b][1].y);
-                    fb[b][3] = widen8(bv[u][b][1].z, bv[u][b][1].w);
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; q++) fb[b][q] = as_bf(bv[u][b][q]);
-                }
+                const size_t piece = (((size_t)(jb + b) * nch + ch) * BW + p) * 64 + lane;
+                bv[slot][b][p] = !bok[b] ? make_uint4(0u, 0u, 0u, 0u)
+                                 : XB_   ? *(const uint4 *)((const uint8_t *)bt + piece * 16)
+                                         : *(const uint4 *)((const uint16_t *)bt + piece * 8);
             }
+    };
+    auto seq = [&](int k) { return c0 + (k + rot) % nc; };   // the chunk walk starts at chunk `rot`
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+    for (int u = 0; u + 1 < RING; u++)
+        if (u < nc) load(u, seq(u));
+    for (int k0 = 0; k0 < nc; k0 += RING) {
 #pragma unroll
-                for (int i = 0; i < NA_; i++)
+        for (int u = 0; u < RING; u++) {
+            const int k = k0 + u;
+            if (k < nc) {
+                if (k + RING - 1 < nc) load((u + RING - 1) % RING, seq(k + RING - 1));
+                bf16x8 fb[NB_][4];
 #pragma unroll
-                    for (int b = 0; b < NB_; b++) acc[i][b] = mfma(as_bf(av[u][i][q]), fb[b][q], acc[i][b]);
+                for (int b = 0; b < NB_; b++) {
+                    if (XB_) {
+                        fb[b][0] = widen8(bv[u][b][0].x, bv[u][b][0].y);
+                        fb[b][1] = widen8(bv[u][b][0].z, bv[u][b][0].w);
+                        fb[b][2] = widen8(bv[u][b][1].x, bv[u][b][1].y);
+                        fb[b][3] = widen8(bv[u][b][1].z, bv[u][b][1].w);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) fb[b][q] = as_bf(bv[u][b][q]);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+#pragma unroll
+                    for (int i = 0; i < NA_; i++)
+#pragma unroll
+                        for (int b = 0; b < NB_; b++) acc[i][b] = mfma(as_bf(av[u][i][q]), fb[b][q], acc[i][b]);
+            }
         }
     }
 }
 
-// Grouped launch: [dW1 tiles: NT1 column tiles x S1 splits][dW2: 4 x S1][dW3: S3 splits].
+// Grouped launch: [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW2][dW3: mb/KW2].
 // dW1[n1][f] = sum_m dh1[m][n1] x[m][f]; dW2[n2][n1] = sum_m dh2[m][n2] h1[m][n1];
-// dW3[j][n] = sum_m dz[m][j] h2[m][n]. Each writes fp32 partials [split][rows][cols].
-__global__ __launch_bounds__(256) void k_wgrad(D1PPOStep a, Work w) {
+// dW3[j][n] = sum_m dz[m][j] h2[m][n]. Each writes fp32 partials [split][rows][cols]. The
+// dW1 splits of one column tile are consecutive blocks, which a launch spreads over the
+// eight XCDs, so each XCD's L2 serves one sample range of dh1 to every column tile.
+__global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
     if (!cursor_ok(a)) return;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lr = lane & 31, lh = lane >> 5;
-    const int mb = a.mb, s1 = mb / KW;
+    const int mb = a.mb, nch = mb / 64, s1 = mb / KW, s2 = mb / KW2;
     int b = blockIdx.x;
     if (b < NT1 * s1) {
-        const int tile = b % NT1, split = b / NT1;
+        const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
-        wgrad_tile<2, 2, true, 4>(w.dh1t, H, 64 * wave, w.xt, K1, 64 * tile, mb, split * KW, KW, acc);
+        wgrad_tile<2, 2, true, 3>(w.dh1f, 2 * wave, 8, 32, w.xf, 2 * tile, XB, nch, split * (KW / 64), KW / 64,
+                                  tile % (KW / 64), acc);
         float *out = w.part1 + (size_t)split * H * K1;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
@@ -470,11 +526,11 @@ __global__ __launch_bounds__(256) void k_wgrad(D1PPOStep a, Work w) {
         return;
     }
     b -= NT1 * s1;
-    if (b < 4 * s1) {
-        const int tile = b % 4, split = b / 4;
+    if (b < 4 * s2) {
+        const int tile = b / s2, split = b % s2;
         floatx16 acc[2][2] = {};
-        wgrad_tile<2, 2, false, 2>(w.dh2t, H, 64 * wave, w.h1t, H, 64 * tile, mb,
-                                   split * KW, KW, acc);
+        wgrad_tile<2, 2, false, 2>(w.dh2f, 2 * wave, 8, 32, w.h1f, 2 * tile, 8, nch, split * (KW2 / 64), KW2 / 64,
+                                   2 * tile, acc);
         float *out = w.part2 + (size_t)split * H * H;
 #pragma unroll
         for (int i = 0; i < 2; i++)
@@ -485,9 +541,9 @@ __global__ __launch_bounds__(256) void k_wgrad(D1PPOStep a, Work w) {
                     out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * H + 64 * tile + 32 * bb + lr] = acc[i][bb][r];
         return;
     }
-    b -= 4 * s1;
+    b -= 4 * s2;
     floatx16 acc[1][2] = {};
-    wgrad_tile<1, 2, false, 4>(w.dzt, NZ, 0, w.h2t, H, 64 * wave, mb, b * KW3, KW3, acc);
+    wgrad_tile<1, 2, false, 3>(w.dzf, 0, 1, NZ, w.h2f, 2 * wave, 8, nch, b * (KW2 / 64), KW2 / 64, 0, acc);
     float *out = w.part3 + (size_t)b * NZ * H;
 #pragma unroll
     for (int bb = 0; bb < 2; bb++)
@@ -499,14 +555,14 @@ __global__ __launch_bounds__(256) void k_wgrad(D1PPOStep a, Work w) {
 }
 
 // ---------------------------------------------------------------- k_reduce
-__device__ __forceinline__ float block_sum(float x, float *red) {
-    red[threadIdx.x] = x;
+__device__ __forceinline__ float block_sum(float x, float *red) {   // 256 lanes, red[4]
+#pragma unroll
+    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
     __syncthreads();
-    for (int o = blockDim.x / 2; o; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    return red[0];
+    const float s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return s;
 }
 
 __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
@@ -517,7 +573,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
         if (ok) a.step[1] = a.step[0] + 1.f;
     }
     if (!ok) return;
-    const int t = threadIdx.x, mb = a.mb, s1 = mb / KW, s3 = mb / KW3;
+    const int t = threadIdx.x, mb = a.mb, s1 = mb / KW, s2 = mb / KW2;
     uint16_t *g = (uint16_t *)a.g;
     float sq = 0.f;
     if (blockIdx.x < NRED) {
@@ -531,10 +587,10 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
                 src = w.part1 + 4 * (size_t)u, S = s1, stride = (size_t)H * K1, dst = g + a.off_w1 + 4 * (size_t)u;
             } else if (u < U1 + U2) {
                 const int e = u - U1;
-                src = w.part2 + 4 * e, S = s1, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
+                src = w.part2 + 4 * e, S = s2, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
             } else {
                 const int e = u - U1 - U2;
-                src = w.part3 + 4 * e, S = s3, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
+                src = w.part3 + 4 * e, S = s2, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
             }
             float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
             for (int q0 = 0; q0 < S; q0 += 8) {   // eight loads in flight, summed in split order
@@ -549,38 +605,80 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
             *(uint2 *)dst = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2 | ((uint32_t)h3 << 16));
             sq += bf(h0) * bf(h0) + bf(h1) * bf(h1) + bf(h2) * bf(h2) + bf(h3) * bf(h3);
         }
-    } else {   // biases: 64 columns per workgroup, 4 lanes per column over the row partials
-        const int col = 64 * (blockIdx.x - NRED) + (t & 63), part = t >> 6, nrows = mb / R;
+    } else {   // biases: 8 columns per workgroup, 32 lanes per column over the row partials
+        const int col = 8 * (blockIdx.x - NRED) + (t >> 5), part = t & 31, nrows = mb / R;
         float s = 0.f;
         if (col < 2 * H + NZ)
-            for (int r0 = part; r0 < nrows; r0 += 32) {   // eight loads in flight
+            for (int r0 = part; r0 < nrows; r0 += 256) {   // eight loads in flight
                 float x[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[j] = r0 + 4 * j < nrows ? w.bpart[(size_t)(r0 + 4 * j) * BP + col] : 0.f;
+                for (int j = 0; j < 8; j++) x[j] = r0 + 32 * j < nrows ? w.bpart[(size_t)(r0 + 32 * j) * BP + col] : 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) s += x[j];
             }
-        red[t] = s;
-        __syncthreads();
-        if (t < 64 && col < 2 * H + NZ) {
-            const uint16_t hb = rb(red[t] + red[t + 64] + red[t + 128] + red[t + 192]);
+#pragma unroll
+        for (int o = 16; o; o >>= 1) s += __shfl_xor(s, o, 32);   // the column's 32 lanes, fixed order
+        if (part == 0 && col < 2 * H + NZ) {
+            const uint16_t hb = rb(s);
             uint16_t *dst = col < H ? g + a.off_b1 + col : col < 2 * H ? g + a.off_b2 + (col - H) : g + a.off_b3 + (col - 2 * H);
             *dst = hb;
             sq = bf(hb) * bf(hb);
         }
-        __syncthreads();
     }
     const float tot = block_sum(sq, red);
     if (t == 0) w.npart[blockIdx.x] = tot;
 }
 
 // ---------------------------------------------------------------- k_adam
+// Refresh the packed slots of flat parameters i0..i0+3 (i0 - each weight offset is a
+// multiple of 4, so the four share a weight row and one 8-byte run of the row-ordered copies).
+__device__ __forceinline__ void pack_param4(const D1PPOStep &a, uint16_t *wpk, int64_t i0, const uint16_t (&h)[4]) {
+    const uint2 v = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    int64_t e;
+    if ((e = i0 - a.off_w1) >= 0 && e < (int64_t)H * K1) {
+        const int n = (int)e / K1, k = (int)e - n * K1;
+        *(uint2 *)(wpk + pk_w1(n, k)) = v;
+    } else if ((e = i0 - a.off_w2) >= 0 && e < H * H) {
+        const int n = (int)e >> 8, k = (int)e & 255;
+        *(uint2 *)(wpk + pk_w2(n, k)) = v;
+#pragma unroll
+        for (int q = 0; q < 4; q++) wpk[pk_w2t(n, k + q)] = h[q];
+    } else if ((e = i0 - a.off_w3) >= 0 && e < NZ * H) {
+        const int j = (int)e >> 8, k = (int)e & 255;
+        *(uint2 *)(wpk + pk_w3(j, k)) = v;
+#pragma unroll
+        for (int q = 0; q < 4; q++) wpk[pk_w3t(j, k + q)] = h[q];
+    }
+}
+// Refresh every packed slot of flat parameter i with its bf16 value h.
+__device__ __forceinline__ void pack_param(const D1PPOStep &a, uint16_t *wpk, int64_t i, uint16_t h) {
+    int64_t e;
+    if ((e = i - a.off_w1) >= 0 && e < (int64_t)H * K1) {
+        wpk[pk_w1((int)e / K1, (int)e % K1)] = h;
+    } else if ((e = i - a.off_w2) >= 0 && e < H * H) {
+        wpk[pk_w2((int)(e >> 8), (int)(e & 255))] = h;
+        wpk[pk_w2t((int)(e >> 8), (int)(e & 255))] = h;
+    } else if ((e = i - a.off_w3) >= 0 && e < NZ * H) {
+        wpk[pk_w3((int)(e >> 8), (int)(e & 255))] = h;
+        wpk[pk_w3t((int)(e >> 8), (int)(e & 255))] = h;
+    }
+}
+
 // Global-norm clip + Adam (torch.optim.Adam, no weight decay) over the flat buffers. Every
 // workgroup re-sums the norm partials; t = step[1] (set by k_reduce); workgroup 0 stores it
 // back to step[0] and advances the minibatch cursor.
 __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
-    __shared__ float red[256];
+    __shared__ float red[4];
     if (a.cursor[1] == 0) return;
+    const uint16_t *g = (const uint16_t *)a.g;
+    uint16_t *pb = (uint16_t *)a.pb;
+    // this lane's four parameters (launched with one group per lane), loaded before the
+    // norm reduction so that both latencies overlap
+    const int64_t i0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    const bool mine = i0 < a.nparams;
+    const int64_t il = mine ? i0 : 0;
+    const uint2 gv = *(const uint2 *)(g + il);
+    float4 pv = *(const float4 *)(a.p + il), mv = *(const float4 *)(a.m + il), vv = *(const float4 *)(a.v + il);
     float acc = 0.f;
     for (int j = threadIdx.x; j < NRED + NBIASB; j += blockDim.x) acc += w.npart[j];
     const float norm = sqrtf(block_sum(acc, red));
@@ -588,13 +686,7 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     const float tt = a.step[1];
     const float bc1 = 1.f - powf(a.beta1, tt), bc2 = 1.f - powf(a.beta2, tt);
     const float step_size = a.lr / bc1, bc2s = sqrtf(bc2);
-    const uint16_t *g = (const uint16_t *)a.g;
-    uint16_t *pb = (uint16_t *)a.pb, *w2t = (uint16_t *)a.w2t, *w3t = (uint16_t *)a.w3t;
-    for (int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 4 * i4 < a.nparams;
-         i4 += (int64_t)gridDim.x * blockDim.x) {   // four parameters per lane
-        const int64_t i0 = 4 * i4;
-        const uint2 gv = *(const uint2 *)(g + i0);
-        float4 pv = *(const float4 *)(a.p + i0), mv = *(const float4 *)(a.m + i0), vv = *(const float4 *)(a.v + i0);
+    if (mine) {
         const float gs[4] = {bf((uint16_t)gv.x), bf((uint16_t)(gv.x >> 16)), bf((uint16_t)gv.y), bf((uint16_t)(gv.y >> 16))};
         float *pp = &pv.x, *mm = &mv.x, *vq = &vv.x;
         uint16_t h[4];
@@ -610,12 +702,7 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
         *(float4 *)(a.m + i0) = mv;
         *(float4 *)(a.v + i0) = vv;
         *(uint2 *)(pb + i0) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int64_t e2 = i0 + e - a.off_w2, e3 = i0 + e - a.off_w3;
-            if (e2 >= 0 && e2 < H * H) w2t[(e2 & (H - 1)) * H + (e2 >> 8)] = h[e];
-            if (e3 >= 0 && e3 < NZ * H) w3t[(e3 & (H - 1)) * 32 + (e3 >> 8)] = h[e];
-        }
+        pack_param4(a, w.wpk, i0, h);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         a.step[0] = tt;
@@ -623,8 +710,19 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     }
 }
 
+// d1_ppo_prepare: zero the packed copies (their padding slots stay zero), then pack every
+// weight from pb.
+__global__ __launch_bounds__(256) void k_pack_zero(uint16_t *wpk) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < P_END; i += gridDim.x * blockDim.x) wpk[i] = 0;
+}
+__global__ __launch_bounds__(256) void k_pack(D1PPOStep a, uint16_t *wpk) {
+    const uint16_t *pb = (const uint16_t *)a.pb;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.nparams; i += (int64_t)gridDim.x * blockDim.x)
+        pack_param(a, wpk, i, pb[i]);
+}
+
 struct Layout {
-    size_t h1t, h2t, dh2t, dh1t, dzt, xt, bpart, part1, part2, part3, npart, total;
+    size_t wpk, h1f, h2f, dh2f, dh1f, dzf, xf, bpart, part1, part2, part3, npart, total;
 };
 static Layout layout(int mb) {
     Layout L{};
@@ -634,20 +732,52 @@ static Layout layout(int mb) {
         off += (bytes + 255) / 256 * 256;
         return at;
     };
-    const size_t s1 = (size_t)mb / KW, s3 = (size_t)mb / KW3;
-    L.h1t = take((size_t)H * mb * 2);
-    L.h2t = take((size_t)H * mb * 2);
-    L.dh2t = take((size_t)H * mb * 2);
-    L.dh1t = take((size_t)H * mb * 2);
-    L.dzt = take((size_t)NZ * mb * 2);
-    L.xt = take((size_t)K1 * mb);
+    L.wpk = take((size_t)P_END * 2);
+    L.h1f = take((size_t)H * mb * 2);
+    L.h2f = take((size_t)H * mb * 2);
+    L.dh2f = take((size_t)H * mb * 2);
+    L.dh1f = take((size_t)H * mb * 2);
+    L.dzf = take((size_t)32 * mb * 2);
+    L.xf = take((size_t)XB * 32 * mb);
     L.bpart = take((size_t)(mb / R) * BP * 4);
-    L.part1 = take(s1 * H * K1 * 4);
-    L.part2 = take(s1 * H * H * 4);
-    L.part3 = take(s3 * NZ * H * 4);
+    L.part1 = take((size_t)(mb / KW) * H * K1 * 4);
+    L.part2 = take((size_t)(mb / KW2) * H * H * 4);
+    L.part3 = take((size_t)(mb / KW2) * NZ * H * 4);
     L.npart = take((size_t)(NRED + NBIASB) * 4);
     L.total = off;
     return L;
+}
+
+static int check_args(const D1PPOStep *s, Work *w) {
+    if (!s) return D1_E_ARG;
+    const D1PPOStep &a = *s;
+    if (a.mb <= 0 || a.mb % KW || a.n < a.mb || a.n >= ((int64_t)1 << 31) || a.nparams % 4) return D1_E_ARG;
+    if (!a.obs || !a.perm || !a.cursor || !a.actions || !a.logp_old || !a.adv || !a.ret || !a.p || !a.pb || !a.g ||
+        !a.m || !a.v || !a.step || !a.loss_parts || !a.work)
+        return D1_E_ARG;
+    if ((uintptr_t)a.obs % 8 || (uintptr_t)a.pb % 16 || (uintptr_t)a.g % 16 || (uintptr_t)a.work % 256 ||
+        (uintptr_t)a.p % 16 || (uintptr_t)a.m % 16 || (uintptr_t)a.v % 16)
+        return D1_E_ARG;
+    const int64_t offs[6] = {a.off_w1, a.off_b1, a.off_w2, a.off_b2, a.off_w3, a.off_b3};
+    const int64_t sizes[6] = {(int64_t)H * K1, H, (int64_t)H * H, H, (int64_t)NZ * H, NZ};
+    for (int i = 0; i < 6; i++)
+        if (offs[i] < 0 || offs[i] % 8 || offs[i] + sizes[i] > a.nparams) return D1_E_ARG;
+    const Layout L = layout(a.mb);
+    if (a.work_bytes < (int64_t)L.total) return D1_E_ARG;
+    char *base = (char *)a.work;
+    w->wpk = (uint16_t *)(base + L.wpk);
+    w->h1f = (uint16_t *)(base + L.h1f);
+    w->h2f = (uint16_t *)(base + L.h2f);
+    w->dh2f = (uint16_t *)(base + L.dh2f);
+    w->dh1f = (uint16_t *)(base + L.dh1f);
+    w->dzf = (uint16_t *)(base + L.dzf);
+    w->xf = (uint8_t *)(base + L.xf);
+    w->bpart = (float *)(base + L.bpart);
+    w->part1 = (float *)(base + L.part1);
+    w->part2 = (float *)(base + L.part2);
+    w->part3 = (float *)(base + L.part3);
+    w->npart = (float *)(base + L.npart);
+    return 0;
 }
 
 }  // namespace d1q
@@ -657,43 +787,27 @@ extern "C" int64_t d1_ppo_work_bytes(int mb) {
     return (int64_t)d1q::layout(mb).total;
 }
 
+extern "C" int d1_ppo_prepare(const D1PPOStep *s, void *stream) {
+    using namespace d1q;
+    Work w;
+    if (int e = check_args(s, &w)) return e;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_pack_zero, dim3(256), dim3(256), 0, st, w.wpk);
+    hipLaunchKernelGGL(k_pack, dim3(512), dim3(256), 0, st, *s, w.wpk);
+    return (int)hipGetLastError();
+}
+
 extern "C" int d1_ppo_step(const D1PPOStep *s, void *stream) {
     using namespace d1q;
-    if (!s) return D1_E_ARG;
-    const D1PPOStep &a = *s;
-    if (a.mb <= 0 || a.mb % KW || a.n < a.mb || a.n >= ((int64_t)1 << 31) || a.nparams % 4) return D1_E_ARG;
-    if (!a.obs || !a.perm || !a.cursor || !a.actions || !a.logp_old || !a.adv || !a.ret || !a.p || !a.pb || !a.g ||
-        !a.m || !a.v || !a.w2t || !a.w3t || !a.step || !a.loss_parts || !a.work)
-        return D1_E_ARG;
-    if ((uintptr_t)a.obs % 8 || (uintptr_t)a.pb % 16 || (uintptr_t)a.g % 16 || (uintptr_t)a.w2t % 16 ||
-        (uintptr_t)a.w3t % 16 || (uintptr_t)a.work % 256 || (uintptr_t)a.p % 16 || (uintptr_t)a.m % 16 ||
-        (uintptr_t)a.v % 16)
-        return D1_E_ARG;
-    const int64_t offs[6] = {a.off_w1, a.off_b1, a.off_w2, a.off_b2, a.off_w3, a.off_b3};
-    const int64_t sizes[6] = {(int64_t)H * K1, H, (int64_t)H * H, H, (int64_t)NZ * H, NZ};
-    for (int i = 0; i < 6; i++)
-        if (offs[i] < 0 || offs[i] % 8 || offs[i] + sizes[i] > a.nparams) return D1_E_ARG;
-    const Layout L = layout(a.mb);
-    if (a.work_bytes < (int64_t)L.total) return D1_E_ARG;
-    char *base = (char *)a.work;
     Work w;
-    w.h1t = (uint16_t *)(base + L.h1t);
-    w.h2t = (uint16_t *)(base + L.h2t);
-    w.dh2t = (uint16_t *)(base + L.dh2t);
-    w.dh1t = (uint16_t *)(base + L.dh1t);
-    w.dzt = (uint16_t *)(base + L.dzt);
-    w.xt = (uint8_t *)(base + L.xt);
-    w.bpart = (float *)(base + L.bpart);
-    w.part1 = (float *)(base + L.part1);
-    w.part2 = (float *)(base + L.part2);
-    w.part3 = (float *)(base + L.part3);
-    w.npart = (float *)(base + L.npart);
-    const int s1 = a.mb / KW, s3 = a.mb / KW3;
+    if (int e = check_args(s, &w)) return e;
+    const D1PPOStep &a = *s;
+    const int s1 = a.mb / KW, s2 = a.mb / KW2;
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(k_rows, dim3(a.mb / R), dim3(512), 0, st, a, w);
-    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1 + s3), dim3(256), 0, st, a, w);
+    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s2 + s2), dim3(256), 0, st, a, w);
     hipLaunchKernelGGL(k_reduce, dim3(NRED + NBIASB), dim3(256), 0, st, a, w);
-    const int64_t nadam = (a.nparams / 4 + 255) / 256;
-    hipLaunchKernelGGL(k_adam, dim3((unsigned)(nadam < NADAM ? nadam : NADAM)), dim3(256), 0, st, a, w);
+    const int64_t nadam = (a.nparams / 4 + 255) / 256;   // one group of four parameters per lane
+    hipLaunchKernelGGL(k_adam, dim3((unsigned)nadam), dim3(256), 0, st, a, w);
     return (int)hipGetLastError();
 }

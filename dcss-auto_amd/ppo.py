@@ -141,10 +141,8 @@ class FastPPO:
         nbytes = _lib.load().d1_ppo_work_bytes(minibatch)
         _lib.check(0 if nbytes > 0 else nbytes, 'd1_ppo_work_bytes')
         self.work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        self.w2t = F.view(F.pb, 'l2.weight').t().contiguous()
-        self.w3t = torch.zeros((256, 32), dtype=torch.bfloat16, device=dev)
-        self.w3t[:, :17] = F.view(F.pb, 'head.weight').t()
         self.perm = None
+        self._packed = False
         self._g = self._g_buf = None
         self._args = self._args_key = None
 
@@ -163,11 +161,14 @@ class FastPPO:
                 n=obs.shape[0], mb=self.minibatch, p=F.p.data_ptr(), pb=F.pb.data_ptr(), g=F.g.data_ptr(),
                 m=F.m.data_ptr(), v=F.v.data_ptr(), nparams=F.n, off_w1=off['l1.weight'], off_b1=off['l1.bias'],
                 off_w2=off['l2.weight'], off_b2=off['l2.bias'], off_w3=off['head.weight'],
-                off_b3=off['head.bias'], w2t=self.w2t.data_ptr(), w3t=self.w3t.data_ptr(),
-                step=self.step_t.data_ptr(), loss_parts=self.loss_parts.data_ptr(), work=self.work.data_ptr(),
+                off_b3=off['head.bias'], step=self.step_t.data_ptr(), loss_parts=self.loss_parts.data_ptr(), work=self.work.data_ptr(),
                 work_bytes=self.work.numel(), clip=self.clip, vcoef=self.vcoef, ecoef=self.ecoef,
                 max_grad_norm=self.max_grad_norm, lr=self.lr, beta1=0.9, beta2=0.999, eps=self.eps)
             self._args_key = key
+        if not self._packed:   # kernel-ordered weight copies in the work buffer, from pb
+            _lib.check(_lib.load().d1_ppo_prepare(self._args, torch.cuda.current_stream(self.dev).cuda_stream),
+                       'd1_ppo_prepare')
+            self._packed = True
         return self._args
 
     def set_order(self, perm):

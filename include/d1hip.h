@@ -177,9 +177,10 @@ int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stre
  *
  * Parameters live in flat buffers (element offsets off_* into p / pb / g / m / v, each a
  * multiple of 8): l1.weight [256,1800], l1.bias [256], l2.weight [256,256], l2.bias [256],
- * head.weight [17,256], head.bias [17] (torch Linear layouts). w2t (bf16 [256][256]) and w3t
- * (bf16 [256][32], columns 17..31 zero) hold l2.weight^T and head.weight^T; the caller fills
- * them once from pb and every call refreshes them with the updated weights. */
+ * head.weight [17,256], head.bias [17] (torch Linear layouts). `work` holds, besides
+ * scratch, copies of the bf16 weights in the order the kernels read them: d1_ppo_prepare
+ * writes them from pb (once before the first step, and again whenever the parameters are
+ * changed outside d1_ppo_step); every step refreshes them with its updated weights. */
 typedef struct {
     const uint8_t *obs;             /* [n, 1800] uint8 observations (8-byte aligned) */
     const int64_t *perm;            /* [n] sample order, entries in [0, n) */
@@ -190,19 +191,19 @@ typedef struct {
     int32_t mb;                     /* minibatch size, a multiple of 1024 */
     int32_t pad0;
     float *p;                       /* fp32 master parameters (16-byte aligned, like every flat buffer) */
-    void *pb;                       /* bf16 copy read by the forward */
+    void *pb;                       /* bf16 copy */
     void *g;                        /* bf16 gradients written by the call */
     float *m, *v;                   /* Adam moments */
-    int64_t nparams;
+    int64_t nparams;                /* a multiple of 4 */
     int64_t off_w1, off_b1, off_w2, off_b2, off_w3, off_b3;
-    void *w2t, *w3t;
     float *step;                    /* [2] Adam step count (torch.optim.Adam semantics, no decay) */
     float *loss_parts;              /* [mb/32 * 4]: per 32 samples the sums of pg, 0.5*(v-R)^2, entropy */
-    void *work;                     /* d1_ppo_work_bytes(mb) bytes of device scratch, 256-byte aligned */
+    void *work;                     /* d1_ppo_work_bytes(mb) bytes of device memory, 256-byte aligned */
     int64_t work_bytes;
     float clip, vcoef, ecoef, max_grad_norm, lr, beta1, beta2, eps;
 } D1PPOStep;
 int64_t d1_ppo_work_bytes(int mb);
+int d1_ppo_prepare(const D1PPOStep *s, void *stream);
 int d1_ppo_step(const D1PPOStep *s, void *stream);
 
 /* Reverse-time GAE over a [T, n] rollout (gpu-d1/scripts/run_ring_ablations.py:354-360):

@@ -16,7 +16,7 @@ def declared_symbols(header='d1hip.h', prefix='d1_'):
 def test_header_declares_the_abi():
     assert declared_symbols() == sorted(['d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size',
                                          'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_gae',
-                                         'd1_obs_to_bf16', 'd1_ppo_work_bytes', 'd1_ppo_step',
+                                         'd1_obs_to_bf16', 'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step',
                                          'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
                                          'd1_sample_ar', 'd1_los_table', 'd1_trunk1'])
     # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
@@ -106,7 +106,7 @@ def test_ppo_step_validation_without_gpu(pkg):
     # 4 activation/gradient arrays [256][mb] + dz [17][mb] (bf16), bias partials, split-K partials
     assert w8k >= 4 * 256 * 8192 * 2 + 8 * 256 * 1800 * 4
     assert L.d1_ppo_work_bytes(4096) < w8k
-    assert L.d1_ppo_step(None, None) == -1
+    assert L.d1_ppo_step(None, None) == -1 and L.d1_ppo_prepare(None, None) == -1
     s = _lib.D1PPOStep(mb=1000, n=4096)
     assert L.d1_ppo_step(C.byref(s), None) == -1                  # minibatch not a multiple of 1024
     s = _lib.D1PPOStep(mb=1024, n=512)

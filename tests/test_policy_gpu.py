@@ -201,11 +201,22 @@ def _small_buffer(T, N, seed=3):
     return buf
 
 
+def _autograd_grads(model, ppo, obs, actions, logp, adv, ret, inds):
+    model.zero_grad(set_to_none=True)
+    with torch.autocast('cuda', dtype=torch.bfloat16):
+        logits, value = model(obs[inds])
+    loss, pg, vl, ent = ppo.ppo_loss(logits, value, actions[inds], logp[inds], adv[inds], ret[inds])
+    loss.backward()
+    return torch.stack([pg, vl, ent]).float()
+
+
 def test_fast_ppo_gradients_match_autograd():
     """The fused minibatch step (libd1hip d1_ppo_step) vs torch autograd under bf16 autocast
     on the same minibatch, taken through a shuffled order: gradients within the bf16 bar
     (2e-2 relative to the gradient scale), loss terms within 2e-2; the Adam step from zero
-    moments (no clipping) moves every weight by lr * g / (|g| + eps), checked to 1e-6."""
+    moments (no clipping) moves every weight by lr * g / (|g| + eps), checked to 1e-6. A
+    second step, after the model takes the updated weights, checks the weight copies the
+    step keeps for its own next call the same way."""
     P = importlib.import_module('dcss-auto_amd.policy')
     ppo = importlib.import_module('dcss-auto_amd.ppo')
     T, N, mb = 4, 4096, 8192
@@ -217,28 +228,20 @@ def test_fast_ppo_gradients_match_autograd():
     obs, actions, logp = fast._views(buf)
     perm = torch.randperm(T * N, device='cuda', generator=torch.Generator(device='cuda').manual_seed(1))
     fast.set_order(perm)
-    fast._step(obs, actions, logp, adv, ret)
-    assert fast.cursor[0].item() == 1
-    inds = perm[:mb]
-    with torch.autocast('cuda', dtype=torch.bfloat16):
-        logits, value = model(obs[inds])
-    loss, pg, vl, ent = ppo.ppo_loss(logits, value, actions[inds], logp[inds], adv[inds], ret[inds])
-    loss.backward()
-    terms = fast.loss_terms()
-    torch.testing.assert_close(terms, torch.stack([pg, vl, ent]).float(), rtol=2e-2, atol=1e-4)
-    for name, prm in model.named_parameters():
-        g = fast.flat.view(fast.flat.g, name).float()
-        scale = prm.grad.abs().max().item() + 1e-12
-        err = (g - prm.grad).abs().max().item() / scale
-        assert err < 2e-2, (name, err)
-    g = fast.flat.g.float()
-    want = p0 - fast.lr * g / (g.abs() + fast.eps)
-    torch.testing.assert_close(fast.flat.p, want, rtol=0, atol=1e-6)
-    for name in ('l2.weight', 'head.weight'):   # the transposed copies the next step reads
-        w = fast.flat.view(fast.flat.pb, name)
-        got = fast.w2t if name == 'l2.weight' else fast.w3t[:, :17]
-        assert torch.equal(got, w.t())
-    assert not fast.w3t[:, 17:].any()
+    for step in range(2):
+        fast._step(obs, actions, logp, adv, ret)
+        assert fast.cursor[0].item() == step + 1
+        want = _autograd_grads(model, ppo, obs, actions, logp, adv, ret, perm[step * mb:(step + 1) * mb])
+        torch.testing.assert_close(fast.loss_terms(), want, rtol=2e-2, atol=1e-4)
+        for name, prm in model.named_parameters():
+            g = fast.flat.view(fast.flat.g, name).float()
+            scale = prm.grad.abs().max().item() + 1e-12
+            err = (g - prm.grad).abs().max().item() / scale
+            assert err < 2e-2, (step, name, err)
+        if step == 0:
+            g = fast.flat.g.float()
+            torch.testing.assert_close(fast.flat.p, p0 - fast.lr * g / (g.abs() + fast.eps), rtol=0, atol=1e-6)
+            fast.flat.load_into(model)
 
 
 def test_fast_ppo_graph_replays_match_eager():
