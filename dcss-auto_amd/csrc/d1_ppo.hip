@@ -39,6 +39,7 @@ namespace d1q {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // register-resident 16-byte piece
 
 constexpr int K1 = 1800;              // observation bytes = layer-1 inputs
 constexpr int H = 256;                // hidden width
@@ -51,8 +52,8 @@ constexpr int XR = K1 + 16;           // LDS row stride (bf16) of k_rows' x tile
 constexpr int BP = 544;               // bias partial row: db1[256] | db2[256] | db3[17] | pad
 constexpr int C1 = 29;                // layer-1 K chunks (28 of 64 + the 8 inputs 1792..1799)
 constexpr int XB = 57;                // 32-row blocks of the x copy (1824 rows, 1800..1823 zero)
-constexpr int KW = 1024;              // samples per dW1 workgroup
-constexpr int KW2 = 512;              // samples per dW2 / dW3 workgroup
+constexpr int KW = 1024;              // samples per dW1 / dW2 workgroup
+constexpr int KW2 = 512;              // samples per dW3 workgroup
 constexpr int NT1 = 29;               // dW1 column tiles of 64 (the last one holds 8 columns)
 constexpr int NRED = (H * K1 + H * H + NZ * H) / 4 / 256 + 1;   // k_reduce weight workgroups: one unit per lane
 constexpr int NBIASB = (2 * H + NZ + 7) / 8;     // k_reduce bias workgroups (8 columns x 32 lanes each)
@@ -71,7 +72,7 @@ struct Work {
     uint16_t *dzf;                       // [32 rows (17 used)][mb] bf16, fragment order
     uint8_t *xf;                         // [1824 rows][mb] uint8 x^T, 16-byte fragment order
     float *bpart;                        // [mb/32][BP]
-    float *part1, *part2, *part3;        // [mb/KW][256][1800], [mb/KW2][256][256], [mb/KW2][17][256]
+    float *part1, *part2, *part3;        // [mb/KW][256][1800], [mb/KW][256][256], [mb/KW2][17][256]
     float *npart;                        // [NRED + NBIASB] sum-of-squares partials
 };
 
@@ -431,48 +432,41 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
 // One split-K tile of out[i][j] = sum_m at[i][m] bt[j][m] over the sample chunks
 // [c0, c0 + nc): both operands fragment-ordered with `nch` chunks; `at` bf16, `bt` bf16 or
 // (XB_) the uint8 x copy. Wave w owns NA_ row blocks of 32 from row block ib, the workgroup
-// NB_ column blocks from jb; row blocks at or past an / bn, and rows >= arows_last within
-// the last A block, read as zero. Loads run through a RING-deep register ring (issued
-// RING-1 chunks ahead); the walk over the chunks starts at chunk c0 + rot and wraps, so
-// that tiles reading the same operand rows at the same time read different chunks.
+// NB_ column blocks from jb. Loads run through a RING-deep register ring (issued RING-1
+// chunks ahead).
 template <int NA_, int NB_, bool XB_, int RING>
-__device__ __forceinline__ void wgrad_tile(const uint16_t *at, int ib, int an, int arows_last, const void *bt, int jb,
-                                           int bn, int nch, int c0, int nc, int rot, floatx16 (&acc)[NA_][NB_]) {
+__device__ __forceinline__ void wgrad_tile(const uint16_t *at, int ib, int an, const void *bt, int jb, int bn, int nch,
+                                           int c0, int nc, floatx16 (&acc)[NA_][NB_]) {
     constexpr int BW = XB_ ? 2 : 4;   // 16-byte pieces per B row block and chunk
     const int lane = threadIdx.x & 63, lr = lane & 31;
-    bool aok[NA_], bok[NB_];
-#pragma unroll
-    for (int i = 0; i < NA_; i++) aok[i] = ib + i < an && (ib + i < an - 1 || lr < arows_last);
-#pragma unroll
-    for (int b = 0; b < NB_; b++) bok[b] = jb + b < bn;
+    // Row / column blocks past an / bn are read from the last block (in bounds): like the
+    // unwritten rows of a block, they only feed outputs that the caller never stores.
     uint4 av[RING][NA_][4], bv[RING][NB_][BW];
     auto load = [&](int slot, int ch) {
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
             for (int i = 0; i < NA_; i++)
-                av[slot][i][q] = aok[i] ? *(const uint4 *)(at + ((((size_t)(ib + i) * nch + ch) * 4 + q) * 64 + lane) * 8)
-                                        : make_uint4(0u, 0u, 0u, 0u);
+                av[slot][i][q] = *(const uint4 *)(at + ((((size_t)min(ib + i, an - 1) * nch + ch) * 4 + q) * 64 + lane) * 8);
 #pragma unroll
         for (int p = 0; p < BW; p++)
 #pragma unroll
             for (int b = 0; b < NB_; b++) {
-                const size_t piece = (((size_t)(jb + b) * nch + ch) * BW + p) * 64 + lane;
-                bv[slot][b][p] = !bok[b] ? make_uint4(0u, 0u, 0u, 0u)
-                                 : XB_   ? *(const uint4 *)((const uint8_t *)bt + piece * 16)
-                                         : *(const uint4 *)((const uint16_t *)bt + piece * 8);
+                const size_t piece = (((size_t)min(jb + b, bn - 1) * nch + ch) * BW + p) * 64 + lane;
+                bv[slot][b][p] = XB_ ? *(const uint4 *)((const uint8_t *)bt + piece * 16)
+                                     : *(const uint4 *)((const uint16_t *)bt + piece * 8);
             }
     };
-    auto seq = [&](int k) { return c0 + (k + rot) % nc; };   // the chunk walk starts at chunk `rot`
 #pragma unroll
     for (int u = 0; u + 1 < RING; u++)
-        if (u < nc) load(u, seq(u));
+        if (u < nc) load(u, c0 + u);
+#pragma unroll 1
     for (int k0 = 0; k0 < nc; k0 += RING) {
 #pragma unroll
         for (int u = 0; u < RING; u++) {
             const int k = k0 + u;
             if (k < nc) {
-                if (k + RING - 1 < nc) load((u + RING - 1) % RING, seq(k + RING - 1));
+                if (k + RING - 1 < nc) load((u + RING - 1) % RING, c0 + k + RING - 1);
                 bf16x8 fb[NB_][4];
 #pragma unroll
                 for (int b = 0; b < NB_; b++) {
@@ -497,21 +491,92 @@ __device__ __forceinline__ void wgrad_tile(const uint16_t *at, int ib, int an, i
     }
 }
 
-// Grouped launch: [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW2][dW3: mb/KW2].
+// The dW1 / dW2 tile: wave w owns A row blocks 2w, 2w+1 (64 rows of `at`), and the four
+// waves share column blocks jb, jb+1 of `bt`. The shared B chunk is loaded once per
+// workgroup (one or two 16-byte pieces per lane; uint8 widened once), staged as fragments
+// in a double-buffered LDS tile `bl` ([2][2 blocks][4 steps][64] of 16 bytes) and read by
+// all four waves. A and B loads run two chunks ahead through three named register slots
+// (chunk c lives in slot c % 3); one barrier per chunk. Column blocks past bn are read
+// from block bn-1 (in bounds): they only feed output columns that the caller never stores,
+// and the loads stay free of branches.
+template <bool XB_>
+__device__ __forceinline__ void wgrad_tile2(const uint16_t *at, const void *bt, int jb, int bn, int nch, int c0, int nc,
+                                            uint4 *bl, floatx16 (&acc)[2][2]) {
+    constexpr int BPL = XB_ ? 1 : 2;   // B pieces per lane and chunk
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int bb = t >> 7, ph = (t >> 6) & 1;    // this lane's B block and half of the four steps
+    const int brow = min(jb + bb, bn - 1);
+    // per-lane base addresses; chunk ch adds ch * 4 KB (A, bf16) or ch * 2 or 4 KB (B)
+    const uint4 *a0 = (const uint4 *)at + (size_t)(2 * wave) * nch * 256 + lane;
+    const uint4 *a1 = a0 + (size_t)nch * 256;
+    const u32x4 *b0 = (const u32x4 *)bt + ((size_t)brow * nch * (XB_ ? 2 : 4) + (XB_ ? ph : 2 * ph)) * 64 + lane;
+    uint4 aS0[2][4], aS1[2][4], aS2[2][4];
+    u32x4 bS0[BPL], bS1[BPL], bS2[BPL];
+    auto load = [&](uint4 (&av)[2][4], u32x4 (&bv)[BPL], int ch) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            av[0][q] = a0[ch * 256 + q * 64];
+            av[1][q] = a1[ch * 256 + q * 64];
+        }
+#pragma unroll
+        for (int e = 0; e < BPL; e++) bv[e] = b0[ch * (XB_ ? 128 : 256) + e * 64];
+    };
+    auto bstore = [&](const u32x4 (&bv)[BPL], int buf) {   // fragments q = 2ph, 2ph + 1 of block bb
+        u32x4 *dst = (u32x4 *)bl + ((buf * 2 + bb) * 4 + 2 * ph) * 64 + lane;
+        if (XB_) {
+            dst[0] = __builtin_bit_cast(u32x4, widen8(bv[0].x, bv[0].y));
+            dst[64] = __builtin_bit_cast(u32x4, widen8(bv[0].z, bv[0].w));
+        } else {
+            dst[0] = bv[0];
+            dst[64] = bv[BPL - 1];
+        }
+    };
+    // chunk k: issue chunk k+2's loads into the slot chunk k-1 used, multiply, stage chunk
+    // k+1's B (loaded two chunks ago) into the other LDS buffer
+    auto step = [&](const uint4 (&acur)[2][4], uint4 (&anext)[2][4], u32x4 (&bnext)[BPL], const u32x4 (&bstage)[BPL],
+                    int k) {
+        if (k + 2 < nc) load(anext, bnext, c0 + k + 2);
+        const uint4 *src = bl + (k & 1) * 2 * 4 * 64 + lane;
+        bf16x8 fb[2][4];
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) fb[b][q] = as_bf(src[(b * 4 + q) * 64]);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) acc[i][b] = mfma(as_bf(acur[i][q]), fb[b][q], acc[i][b]);
+        if (k + 1 < nc) bstore(bstage, (k + 1) & 1);
+        __syncthreads();
+    };
+    load(aS0, bS0, c0);
+    if (nc > 1) load(aS1, bS1, c0 + 1);
+    bstore(bS0, 0);
+    __syncthreads();
+    for (int k0 = 0; k0 < nc; k0 += 3) {
+        step(aS0, aS2, bS2, bS1, k0);
+        if (k0 + 1 < nc) step(aS1, aS0, bS0, bS2, k0 + 1);
+        if (k0 + 2 < nc) step(aS2, aS1, bS1, bS0, k0 + 2);
+    }
+}
+
+// Grouped launch: [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW][dW3: mb/KW2].
 // dW1[n1][f] = sum_m dh1[m][n1] x[m][f]; dW2[n2][n1] = sum_m dh2[m][n2] h1[m][n1];
 // dW3[j][n] = sum_m dz[m][j] h2[m][n]. Each writes fp32 partials [split][rows][cols]. The
 // dW1 splits of one column tile are consecutive blocks, which a launch spreads over the
 // eight XCDs, so each XCD's L2 serves one sample range of dh1 to every column tile.
 __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
+    __shared__ uint4 bl[2 * 2 * 4 * 64];
     if (!cursor_ok(a)) return;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lr = lane & 31, lh = lane >> 5;
-    const int mb = a.mb, nch = mb / 64, s1 = mb / KW, s2 = mb / KW2;
+    const int mb = a.mb, nch = mb / 64, s1 = mb / KW;
     int b = blockIdx.x;
     if (b < NT1 * s1) {
         const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
-        wgrad_tile<2, 2, true, 3>(w.dh1f, 2 * wave, 8, 32, w.xf, 2 * tile, XB, nch, split * (KW / 64), KW / 64,
-                                  tile % (KW / 64), acc);
+        wgrad_tile2<true>(w.dh1f, w.xf, 2 * tile, XB, nch, split * (KW / 64), KW / 64, bl, acc);
         float *out = w.part1 + (size_t)split * H * K1;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
@@ -526,11 +591,10 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
         return;
     }
     b -= NT1 * s1;
-    if (b < 4 * s2) {
-        const int tile = b / s2, split = b % s2;
+    if (b < 4 * s1) {
+        const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
-        wgrad_tile<2, 2, false, 2>(w.dh2f, 2 * wave, 8, 32, w.h1f, 2 * tile, 8, nch, split * (KW2 / 64), KW2 / 64,
-                                   2 * tile, acc);
+        wgrad_tile2<false>(w.dh2f, w.h1f, 2 * tile, 8, nch, split * (KW / 64), KW / 64, bl, acc);
         float *out = w.part2 + (size_t)split * H * H;
 #pragma unroll
         for (int i = 0; i < 2; i++)
@@ -541,9 +605,9 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
                     out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * H + 64 * tile + 32 * bb + lr] = acc[i][bb][r];
         return;
     }
-    b -= 4 * s2;
+    b -= 4 * s1;
     floatx16 acc[1][2] = {};
-    wgrad_tile<1, 2, false, 3>(w.dzf, 0, 1, NZ, w.h2f, 2 * wave, 8, nch, b * (KW2 / 64), KW2 / 64, 0, acc);
+    wgrad_tile<1, 2, false, 3>(w.dzf, 0, 1, w.h2f, 2 * wave, 8, nch, b * (KW2 / 64), KW2 / 64, acc);
     float *out = w.part3 + (size_t)b * NZ * H;
 #pragma unroll
     for (int bb = 0; bb < 2; bb++)
@@ -587,7 +651,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
                 src = w.part1 + 4 * (size_t)u, S = s1, stride = (size_t)H * K1, dst = g + a.off_w1 + 4 * (size_t)u;
             } else if (u < U1 + U2) {
                 const int e = u - U1;
-                src = w.part2 + 4 * e, S = s2, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
+                src = w.part2 + 4 * e, S = s1, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
             } else {
                 const int e = u - U1 - U2;
                 src = w.part3 + 4 * e, S = s2, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
@@ -741,7 +805,7 @@ static Layout layout(int mb) {
     L.xf = take((size_t)XB * 32 * mb);
     L.bpart = take((size_t)(mb / R) * BP * 4);
     L.part1 = take((size_t)(mb / KW) * H * K1 * 4);
-    L.part2 = take((size_t)(mb / KW2) * H * H * 4);
+    L.part2 = take((size_t)(mb / KW) * H * H * 4);
     L.part3 = take((size_t)(mb / KW2) * NZ * H * 4);
     L.npart = take((size_t)(NRED + NBIASB) * 4);
     L.total = off;
@@ -805,7 +869,7 @@ extern "C" int d1_ppo_step(const D1PPOStep *s, void *stream) {
     const int s1 = a.mb / KW, s2 = a.mb / KW2;
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(k_rows, dim3(a.mb / R), dim3(512), 0, st, a, w);
-    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s2 + s2), dim3(256), 0, st, a, w);
+    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1 + s2), dim3(256), 0, st, a, w);
     hipLaunchKernelGGL(k_reduce, dim3(NRED + NBIASB), dim3(256), 0, st, a, w);
     const int64_t nadam = (a.nparams / 4 + 255) / 256;   // one group of four parameters per lane
     hipLaunchKernelGGL(k_adam, dim3((unsigned)nadam), dim3(256), 0, st, a, w);
