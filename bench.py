@@ -253,6 +253,7 @@ def main():
                          'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer')
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
     ap.add_argument('--eager-ppo', action='store_true', help='run the PPO update without HIP-graph capture')
+    ap.add_argument('--no-ppo', action='store_true', help='rollout mode: skip the C4 PPO measurement that follows')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
@@ -343,6 +344,10 @@ def main():
         'trunk': {'bound': 'mfma', 'achieved': trunk_tflops, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                   'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms},
     }
+    if not args.no_ppo:   # the metric's second number: C4 PPO samples/s, measured after the rollout
+        ppo = ppo_bench(args, env, model, policy_mod, dev)
+        result['ppo'] = {k: ppo[k] for k in ('metric', 'value', 'unit', 'update_s', 'sample_epochs_per_s', 'dtype',
+                                             'path', 'config', 'mfma')}
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline()
     print(json.dumps(result), flush=True)
