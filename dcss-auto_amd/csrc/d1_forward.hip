@@ -1,0 +1,322 @@
+// d1hip: the rollout policy forward as one MFMA kernel for MI355X (gfx950).
+//
+// logits, value = head(relu(relu(obs W1^T + b1) W2^T + b2)) for the BASELINE policy
+// (gpu-d1/scripts/run_ring_ablations.py:209-223 with 1800 -> 256 -> 256 ReLU and a
+// 16-logit + value head): obs uint8 [M, 1800] read directly (every byte value is exact in
+// bf16), bf16 weights packed once per weight update (d1_policy_pack), fp32 accumulation,
+// each layer's output rounded to bf16 where the bf16 torch path rounds it, fp32 logits
+// [M, 16] and value [M] out. One launch replaces the widening pass, three library GEMMs
+// and the dtype copy of the rollout forward.
+//
+// Every layer is computed transposed, D = W x act^T (A operand = weight rows, B operand =
+// 32 samples), so that a lane's D registers hold one sample's hidden units. A 256-lane
+// workgroup owns 256 samples; wave w computes samples 64w..64w+63 as 2 x 8 tiles of 32x32.
+//   layer 1  29 chunks of 64 inputs. Each chunk's W1 fragments (32 KB) are copied once per
+//            workgroup into double-buffered LDS (1 KB contiguous per load instruction);
+//            the observation fragments come straight from global memory two chunks
+//            ahead and are widened to bf16 in registers.
+//   layer 2  h1 never leaves registers: in tile (a, b) lane (l%32, h = l/32) register r
+//            holds hidden unit 32b + 8(r/4) + 4h + r%4 of sample 32a + l%32, and K step s
+//            of layer 2 takes registers 8(s%2)..8(s%2)+7 of tile (a, s/2) as its B operand
+//            slots j = 0..7. Slot j of half h in step s therefore stands for hidden unit
+//            k(s, h, j) = 32(s/2) + 16(s%2) + 8(j/4) + 4h + j%4, and W2 is packed in that
+//            order. W2 and the head weights (144 KB) are staged in LDS once per workgroup.
+//   head     the same for h2 against a 32-row head (rows 17..31 zero).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/d1hip.h"
+#include "d1_frag.h"
+
+namespace d1t {
+
+using namespace d1f;
+
+constexpr int K1 = 1800, H = 256, NA = 16, NZ = 17, BM = 256;
+constexpr int C1 = 29;                       // layer-1 K chunks (28 of 64 + inputs 1792..1799)
+constexpr int PW1 = 0;                       // W1: [29 chunks][8 row blocks][4 steps][64 lanes][8]
+constexpr int PW2 = PW1 + 8 * C1 * 4 * 512;  // W2: [8 row blocks][16 steps][64][8], K order k(s, h, j)
+constexpr int PW3 = PW2 + 8 * 16 * 512;      // head: [16 steps][64][8], rows 17..31 zero
+constexpr int PEND = PW3 + 16 * 512;
+constexpr int NSTAGE = (PEND - PW2) / 8;     // 16-byte pieces of W2 + head staged per workgroup (9216)
+constexpr int LDS_W = NSTAGE * 16;           // 147,456 B (the layer-1 W1 buffers, 64 KB, alias its start)
+constexpr int LDS_BYTES = LDS_W + 2 * 320 * 2;   // + biases b1 | b2 | head bias (padded to 32)
+static_assert(2 * 2048 * 16 <= LDS_W, "W1 double buffer inside the staging area");
+static_assert(NSTAGE % 256 == 0, "whole staging rounds");
+
+// hidden unit of B slot j, lane half h, layer-2/head K step s
+__host__ __device__ constexpr int kperm(int s, int h, int j) {
+    return 32 * (s >> 1) + 16 * (s & 1) + 8 * (j >> 2) + 4 * h + (j & 3);
+}
+
+__global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs, int M, const uint16_t *__restrict__ wpk,
+                                                const uint16_t *__restrict__ b1, const uint16_t *__restrict__ b2,
+                                                const uint16_t *__restrict__ b3, float *__restrict__ logits,
+                                                float *__restrict__ value) {
+    __shared__ __align__(16) uint8_t lds[LDS_BYTES];
+    const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
+    u32x4 *stage = (u32x4 *)lds;                           // W1 double buffer, later W2 + head
+    uint16_t *bl = (uint16_t *)(lds + LDS_W);              // [0,256) b1, [256,512) b2, [512,544) head bias
+    const int m0 = blockIdx.x * BM + 64 * (t >> 6);
+
+    bl[t] = b1[t];
+    bl[256 + t] = b2[t];
+    if (t < 32) bl[512 + t] = t < NZ ? b3[t] : 0;
+
+    floatx16 acc[2][8];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 8; b++) acc[a][b] = floatx16{};
+
+    // ---- layer 1. W1 chunk c (32 KB, contiguous in the packed buffer) is loaded two chunks
+    // ahead into register slot c % 2 (8 pieces of 16 bytes per lane) and stored into LDS
+    // buffer c % 2 one chunk ahead. Observation fragments (sample 32a + lr, bytes
+    // 64ch + 32lh + 8q .. +7) are loaded two chunks ahead into three named register slots
+    // (chunk c in slot c % 3). No load sits behind a branch: samples at or past M read row
+    // M-1 (their outputs are not stored) and the chunk-28 addresses past input 1799 are
+    // clamped to 1792, where the packed W1 is zero.
+    const uint8_t *arow[2];
+#pragma unroll
+    for (int a = 0; a < 2; a++) arow[a] = obs + (size_t)min(m0 + 32 * a + lr, M - 1) * K1;
+    u32x2 vA0[2][4], vA1[2][4], vA2[2][4];
+    u32x4 vb0[8], vb1[8];
+    auto aload = [&](u32x2 (&va)[2][4], int ch) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int k = min(64 * ch + 32 * lh + 8 * q, K1 - 8);
+#pragma unroll
+            for (int a = 0; a < 2; a++) va[a][q] = *(const u32x2 *)(arow[a] + k);
+        }
+    };
+    // pieces t + 256i of chunk ch (row block p >> 8, step (p >> 6) & 3, lane p & 63), stored
+    // at the same piece index of an LDS buffer
+    auto bload = [&](u32x4 (&vb)[8], int ch) {
+        const u32x4 *src = (const u32x4 *)(wpk + PW1) + (size_t)ch * 2048 + t;
+#pragma unroll
+        for (int i = 0; i < 8; i++) vb[i] = src[256 * i];
+    };
+    auto bstore = [&](const u32x4 (&vb)[8], int buf) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) stage[buf * 2048 + t + 256 * i] = vb[i];
+    };
+    // the next step's 8 W1 fragments are read from LDS while this step's 16 MFMAs run
+    auto mma1 = [&](int buf, const bf16x8 (&fa)[2][4]) {
+        const u32x4 *src = stage + buf * 2048 + lane;
+        bf16x8 fw[8], fn[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) fw[b] = as_bf(src[b * 4 * 64]);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (q < 3) {
+#pragma unroll
+                for (int b = 0; b < 8; b++) fn[b] = as_bf(src[(b * 4 + q + 1) * 64]);
+            }
+#pragma unroll
+            for (int b = 0; b < 8; b++)
+#pragma unroll
+                for (int a = 0; a < 2; a++) acc[a][b] = mfma(fw[b], fa[a][q], acc[a][b]);
+            if (q < 3) {
+#pragma unroll
+                for (int b = 0; b < 8; b++) fw[b] = fn[b];
+            }
+        }
+    };
+    // The empty asm makes the slot's value opaque where it is consumed: without it the
+    // compiler computes the widening right behind the load, two chunks early, and waits
+    // for the observation bytes there, which undoes the prefetch.
+    auto widen_slot = [&](u32x2 (&v)[2][4], bf16x8 (&fa)[2][4]) {
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                asm volatile("" : "+v"(v[a][q]));
+                fa[a][q] = widen8(v[a][q].x, v[a][q].y);
+            }
+    };
+    // chunk ch < 28: issue chunk ch + 2's W1 and observation loads (the W1 loads first),
+    // multiply chunk ch, store chunk ch + 1's W1 pieces (loaded a step earlier: loads retire
+    // in issue order, so this waits for them and not for this step's loads) into the other
+    // buffer, meet at the barrier. The scheduling groups pin the order: the first step's 8
+    // fragment reads, the global loads, then 2 MFMAs per LDS read, the LDS stores last.
+    auto step = [&](int ch, u32x2 (&vcur)[2][4], u32x2 (&vnext)[2][4], u32x4 (&vbl)[8], const u32x4 (&vbs)[8],
+                    bool more) {
+        bf16x8 fa[2][4];
+        widen_slot(vcur, fa);
+        if (more) bload(vbl, ch + 2);
+        aload(vnext, ch + 2);
+        mma1(ch & 1, fa);
+        bstore(vbs, (ch + 1) & 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        if (more) __builtin_amdgcn_sched_group_barrier(0x020, 12, 0);
+        else __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 24; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);
+        __syncthreads();
+    };
+    bload(vb0, 0);
+    aload(vA0, 0);
+    bload(vb1, 1);
+    aload(vA1, 1);
+    bstore(vb0, 0);
+    __syncthreads();
+    for (int ch = 0; ch < 24; ch += 6) {   // chunk c: observation slot c % 3, W1 slot c % 2
+        step(ch, vA0, vA2, vb0, vb1, true);
+        step(ch + 1, vA1, vA0, vb1, vb0, true);
+        step(ch + 2, vA2, vA1, vb0, vb1, true);
+        step(ch + 3, vA0, vA2, vb1, vb0, true);
+        step(ch + 4, vA1, vA0, vb0, vb1, true);
+        step(ch + 5, vA2, vA1, vb1, vb0, true);
+    }
+    step(24, vA0, vA2, vb0, vb1, true);
+    step(25, vA1, vA0, vb1, vb0, true);
+    step(26, vA2, vA1, vb0, vb1, true);
+    step(27, vA0, vA2, vb1, vb0, false);   // stores chunk 28's W1 pieces in buffer 0
+    {                                       // chunk 28 (inputs 1792..1799) sits in slot 1
+        bf16x8 fa[2][4];
+        widen_slot(vA1, fa);
+        mma1(0, fa);
+    }
+    __syncthreads();   // every wave is done with the W1 buffers before they are overwritten
+
+    // bias + ReLU + bf16 rounding of acc into B fragments: fragment s of sample block a takes
+    // registers 8(s%2)..+7 of tile (a, s/2); register 4g + i is hidden unit 32b + 8g + 4lh + i
+    bf16x8 hf[2][16];
+    auto to_frags = [&](const uint16_t *bias) {
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const u32x2 bw = *(const u32x2 *)(bias + 32 * b + 8 * g + 4 * lh);
+                const float bb[4] = {bf(bw.x & 0xFFFFu), bf(bw.x >> 16), bf(bw.y & 0xFFFFu), bf(bw.y >> 16)};
+#pragma unroll
+                for (int a = 0; a < 2; a++) {
+                    const int s = 2 * b + (g >> 1), j0 = 4 * (g & 1);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) hf[a][s][j0 + i] = __builtin_bit_cast(__bf16, rb_num(fmaxf(acc[a][b][4 * g + i] + bb[i], 0.f)));
+                }
+            }
+    };
+    // stage W2 + head (contiguous in the packed buffer) into LDS in 3 rounds of 12 pieces;
+    // the h1 conversion runs while the first round is in flight
+    {
+        constexpr int RND = NSTAGE / 256 / 3;
+        u32x4 v[RND];
+        auto sload = [&](int r) {
+#pragma unroll
+            for (int i = 0; i < RND; i++) v[i] = *(const u32x4 *)(wpk + PW2 + (size_t)(t + 256 * (RND * r + i)) * 8);
+        };
+        auto sstore = [&](int r) {
+#pragma unroll
+            for (int i = 0; i < RND; i++) stage[t + 256 * (RND * r + i)] = v[i];
+        };
+        sload(0);
+        to_frags(bl);
+        sstore(0);
+        sload(1);
+        sstore(1);
+        sload(2);
+        sstore(2);
+    }
+    __syncthreads();   // staged weights visible
+
+    // ---- layer 2
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 8; b++) acc[a][b] = floatx16{};
+    {
+        const u32x4 *w2 = stage + lane;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            bf16x8 fw[8];
+#pragma unroll
+            for (int b = 0; b < 8; b++) fw[b] = as_bf(w2[(b * 16 + s) * 64]);
+#pragma unroll
+            for (int b = 0; b < 8; b++)
+#pragma unroll
+                for (int a = 0; a < 2; a++) acc[a][b] = mfma(fw[b], hf[a][s], acc[a][b]);
+        }
+    }
+    to_frags(bl + 256);
+
+    // ---- head: z[a] lane (lr, lh) register r = output 8(r/4) + 4lh + r%4 of sample 32a + lr
+    floatx16 z[2] = {};
+    {
+        const u32x4 *w3 = stage + 8 * 16 * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const bf16x8 fw = as_bf(w3[s * 64]);
+#pragma unroll
+            for (int a = 0; a < 2; a++) z[a] = mfma(fw, hf[a][s], z[a]);
+        }
+    }
+    const uint16_t *b3l = bl + 512;
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+        const int m = m0 + 32 * a + lr;
+        if (m < M) {
+            // the head output is bf16 (rounded once after the bias), widened to fp32
+#pragma unroll
+            for (int g = 0; g < 2; g++) {
+                float4 o;
+                o.x = bf(rb(z[a][4 * g + 0] + bf(b3l[8 * g + 4 * lh + 0])));
+                o.y = bf(rb(z[a][4 * g + 1] + bf(b3l[8 * g + 4 * lh + 1])));
+                o.z = bf(rb(z[a][4 * g + 2] + bf(b3l[8 * g + 4 * lh + 2])));
+                o.w = bf(rb(z[a][4 * g + 3] + bf(b3l[8 * g + 4 * lh + 3])));
+                *(float4 *)(logits + (size_t)m * NA + 8 * g + 4 * lh) = o;
+            }
+            if (lh == 0) value[m] = bf(rb(z[a][8] + bf(b3l[16])));
+        }
+    }
+}
+
+// Packed weights, one thread per element (gather form: every element is written, padding
+// as zero). Element e of a region: j = e & 7, lane = (e >> 3) & 63 (row lane % 32, half
+// lane / 32), step = e >> 9 within the region's block/chunk index.
+__global__ __launch_bounds__(256) void k_policy_pack(const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2,
+                                                     const uint16_t *__restrict__ w3, uint16_t *__restrict__ wpk) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < PEND; e += gridDim.x * blockDim.x) {
+        const int j = e & 7, ln = (e >> 3) & 63, r = ln & 31, h = ln >> 5;
+        uint16_t v = 0;
+        if (e < PW2) {   // W1 [chunk][block][q]: row 32 block + r, input 64 chunk + 32h + 8q + j
+            const int q = (e >> 9) & 3, blk = (e >> 11) & 7, ch = e >> 14;
+            const int k = 64 * ch + 32 * h + 8 * q + j;
+            if (k < K1) v = w1[(size_t)(32 * blk + r) * K1 + k];
+        } else if (e < PW3) {   // W2 [block][s]: row 32 block + r, hidden unit kperm(s, h, j)
+            const int f = e - PW2, s = (f >> 9) & 15, blk = f >> 13;
+            v = w2[(32 * blk + r) * H + kperm(s, h, j)];
+        } else {   // head [s]: output r (< 17), hidden unit kperm(s, h, j)
+            const int s = (e - PW3) >> 9;
+            if (r < NZ) v = w3[r * H + kperm(s, h, j)];
+        }
+        wpk[e] = v;
+    }
+}
+
+}  // namespace d1t
+
+extern "C" int64_t d1_policy_packed_elems(void) { return d1t::PEND; }
+
+extern "C" int d1_policy_pack(const void *w1, const void *w2, const void *w3, void *wpk, void *stream) {
+    if (!w1 || !w2 || !w3 || !wpk || (uintptr_t)wpk % 16) return D1_E_ARG;
+    hipLaunchKernelGGL(d1t::k_policy_pack, dim3((d1t::PEND + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)w1, (const uint16_t *)w2, (const uint16_t *)w3, (uint16_t *)wpk);
+    return (int)hipGetLastError();
+}
+
+extern "C" int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
+                             float *logits, float *value, void *stream) {
+    if (M < 0 || (M > 0 && (!obs || !wpk || !b1 || !b2 || !b3 || !logits || !value))) return D1_E_ARG;
+    if ((uintptr_t)obs % 8 || (uintptr_t)wpk % 16 || (uintptr_t)logits % 16) return D1_E_ARG;
+    if (M == 0) return 0;
+    hipLaunchKernelGGL(d1t::k_policy, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs, M,
+                       (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, logits,
+                       value);
+    return (int)hipGetLastError();
+}

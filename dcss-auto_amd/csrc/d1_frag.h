@@ -1,0 +1,72 @@
+// d1hip: MFMA operand helpers shared by the policy forward (d1_forward.hip) and the PPO step
+// (d1_ppo.hip), gfx950.
+//
+// MFMA: v_mfma_f32_32x32x16_bf16. Lane layouts (checked on the hardware): A lane l holds
+// A[l%32][8(l/32)+j], B lane l holds B[8(l/32)+j][l%32], D lane l holds
+// D[8(r/4)+4(l/32)+r%4][l%32]. The contraction order inside a 64-wide K chunk is free as
+// long as A and B agree, so in chunk c, step q, slot j of a lane in half h stands for
+// k = 64c + 32h + 8q + j: each lane then reads 32 contiguous K values per operand row.
+//
+// Fragment order. An operand that the MFMAs read as [row][k] (32-row block b, K chunk c,
+// step q) is stored so that the 64 lanes' 16-byte pieces of one step are one contiguous
+// kilobyte: element (row, k) at ((((b * nchunks + c) * 4 + q) * 64 + row%32 + 32h) * 8 + j).
+// Every operand load is then one fully used 1 KB span instead of 32 rows x 32 bytes.
+#ifndef D1_FRAG_H
+#define D1_FRAG_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace d1f {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+// register-resident 8- and 16-byte pieces (HIP's uint2/uint4 structs, copied whole through
+// references, can be left in scratch by the compiler; native vectors are not)
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+// float -> bf16, round to nearest even; NaNs stay NaN (quiet bit set when the dropped half
+// held the payload). Branch-free: in the epilogues this runs on hundreds of values per lane.
+__device__ __forceinline__ uint16_t rb(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t n = (u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u);
+    return (uint16_t)((u & 0x7F800000u) == 0x7F800000u ? n : r);
+}
+// the same for inputs known not to be NaN (ReLU outputs: fmaxf(x, 0) never returns NaN);
+// +-inf round to themselves
+__device__ __forceinline__ uint16_t rb_num(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+// two bytes of x (at bit 8s) -> two bf16 in one dword (exact: byte values need 8 bits)
+__device__ __forceinline__ uint32_t widen2(uint32_t x, int s) {
+    uint32_t lo = __float_as_uint((float)((x >> (8 * s)) & 255u)) >> 16;
+    uint32_t hi = __float_as_uint((float)((x >> (8 * s + 8)) & 255u)) & 0xFFFF0000u;
+    return lo | hi;
+}
+// four bytes -> four bf16 (exact): the high halves of the converted floats, paired by v_perm
+__device__ __forceinline__ uint2 widen4(uint32_t x) {
+    const uint32_t f0 = __float_as_uint((float)(x & 255u)), f1 = __float_as_uint((float)((x >> 8) & 255u));
+    const uint32_t f2 = __float_as_uint((float)((x >> 16) & 255u)), f3 = __float_as_uint((float)(x >> 24));
+    return make_uint2(__builtin_amdgcn_perm(f1, f0, 0x07060302u), __builtin_amdgcn_perm(f3, f2, 0x07060302u));
+}
+__device__ __forceinline__ bf16x8 widen8(uint32_t x0, uint32_t x1) {
+    return __builtin_bit_cast(bf16x8, make_uint4(widen2(x0, 0), widen2(x0, 2), widen2(x1, 0), widen2(x1, 2)));
+}
+__device__ __forceinline__ bf16x8 as_bf(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ floatx16 mfma(bf16x8 a, bf16x8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// D row of accumulator register r in lane half h
+__device__ __forceinline__ int drow(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+// fragment-order index of element (row, k) of a [rows][nch*64] bf16 operand
+__device__ __forceinline__ size_t fidx(int row, int k, int nch) {
+    return ((((size_t)(row >> 5) * nch + (k >> 6)) * 4 + ((k >> 3) & 3)) * 64 + (row & 31) + 32 * ((k >> 5) & 1)) * 8 +
+           (k & 7);
+}
+
+}  // namespace d1f
+#endif

@@ -18,28 +18,19 @@
 //   k_adam    global-norm clip + Adam on the fp32 masters, the bf16 copy, the fragment-ordered
 //             weight copies the next k_rows reads, and the minibatch cursor.
 //
-// MFMA: v_mfma_f32_32x32x16_bf16. Lane layouts (checked on the hardware): A lane l holds
-// A[l%32][8(l/32)+j], B lane l holds B[8(l/32)+j][l%32], D lane l holds
-// D[8(r/4)+4(l/32)+r%4][l%32]. The contraction order inside a 64-wide K chunk is free as
-// long as A and B agree, so in chunk c, step q, slot j of a lane in half h stands for
-// k = 64c + 32h + 8q + j.
-//
-// Fragment order. An operand that the MFMAs read as [row][k] (32-row block b, K chunk c,
-// step q) is stored so that the 64 lanes' 16-byte pieces of one step are one contiguous
-// kilobyte: element (row, k) at ((((b * nchunks + c) * 4 + q) * 64 + row%32 + 32h) * 8 + j).
-// Every operand load is then one fully used 1 KB span instead of 32 rows x 32 bytes. The
-// weights are kept in this order by k_adam (and d1_ppo_prepare), the activations and
-// gradients by k_rows; the uint8 x copy uses 16-byte pieces (two per lane and chunk).
+// MFMA operand layouts, the K order inside a chunk and the fragment order are those of
+// d1_frag.h. The weights are kept in fragment order by k_adam (and d1_ppo_prepare), the
+// activations and gradients by k_rows; the uint8 x copy uses 16-byte pieces (two per lane
+// and chunk).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../include/d1hip.h"
+#include "d1_frag.h"
 
 namespace d1q {
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // register-resident 16-byte piece
+using namespace d1f;
 
 constexpr int K1 = 1800;              // observation bytes = layer-1 inputs
 constexpr int H = 256;                // hidden width
@@ -76,45 +67,12 @@ struct Work {
     float *npart;                        // [NRED + NBIASB] sum-of-squares partials
 };
 
-__device__ __forceinline__ float bf(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
-__device__ __forceinline__ uint16_t rb(float f) {   // float -> bf16, round to nearest even
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u) return (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-// two bytes of x (at bit 8s) -> two bf16 in one dword (exact: byte values need 8 bits)
-__device__ __forceinline__ uint32_t widen2(uint32_t x, int s) {
-    uint32_t lo = __float_as_uint((float)((x >> (8 * s)) & 255u)) >> 16;
-    uint32_t hi = __float_as_uint((float)((x >> (8 * s + 8)) & 255u)) & 0xFFFF0000u;
-    return lo | hi;
-}
-// four bytes -> four bf16 (exact): the high halves of the converted floats, paired by v_perm
-__device__ __forceinline__ uint2 widen4(uint32_t x) {
-    const uint32_t f0 = __float_as_uint((float)(x & 255u)), f1 = __float_as_uint((float)((x >> 8) & 255u));
-    const uint32_t f2 = __float_as_uint((float)((x >> 16) & 255u)), f3 = __float_as_uint((float)(x >> 24));
-    return make_uint2(__builtin_amdgcn_perm(f1, f0, 0x07060302u), __builtin_amdgcn_perm(f3, f2, 0x07060302u));
-}
-__device__ __forceinline__ bf16x8 widen8(uint32_t x0, uint32_t x1) {
-    return __builtin_bit_cast(bf16x8, make_uint4(widen2(x0, 0), widen2(x0, 2), widen2(x1, 0), widen2(x1, 2)));
-}
-__device__ __forceinline__ bf16x8 as_bf(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
-__device__ __forceinline__ floatx16 mfma(bf16x8 a, bf16x8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ int64_t clamp_index(int64_t s, int64_t n) { return s < 0 ? 0 : (s >= n ? n - 1 : s); }
 __device__ __forceinline__ bool cursor_ok(const D1PPOStep &a) {
     const int cur = a.cursor[0];
     return cur >= 0 && (int64_t)(cur + 1) * a.mb <= a.n;
 }
-// D row of accumulator register r in lane half h
-__device__ __forceinline__ int drow(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
-// fragment-order index of element (row, k) of a [rows][nch*64] bf16 operand
-__device__ __forceinline__ size_t fidx(int row, int k, int nch) {
-    return ((((size_t)(row >> 5) * nch + (k >> 6)) * 4 + ((k >> 3) & 3)) * 64 + (row & 31) + 32 * ((k >> 5) & 1)) * 8 +
-           (k & 7);
-}
-// the same for the uint8 x copy: 16-byte pieces, two per lane and chunk
+// fragment order for the uint8 x copy: 16-byte pieces, two per lane and chunk
 __device__ __forceinline__ size_t xidx(int row, int k, int nch) {
     return ((((size_t)(row >> 5) * nch + (k >> 6)) * 2 + ((k >> 4) & 1)) * 64 + (row & 31) + 32 * ((k >> 5) & 1)) * 16 +
            (k & 15);

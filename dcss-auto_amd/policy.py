@@ -3,9 +3,10 @@ and a scalar value head, plus the counter-RNG categorical sampler and GAE kernel
 
 The reference's policy is an fp32 MLP with tanh and orthogonal init
 (gpu-d1/scripts/run_ring_ablations.py:209-223); this one follows BASELINE's C3
-architecture: N(0, 0.02) weights, zero biases. The trunk GEMMs run on hipBLASLt
-through torch in bf16 with fp32 accumulation; sampling and GAE are HIP kernels in
-libd1hip.so.
+architecture: N(0, 0.02) weights, zero biases. The bf16 inference forward on uint8
+observations (the rollout's) is one HIP MFMA kernel in libd1hip.so (d1_policy_fwd) on
+weights packed once per update; other dtypes and the autograd path use torch. Sampling and
+GAE are HIP kernels in libd1hip.so.
 """
 import torch
 from torch import nn
@@ -36,12 +37,8 @@ class Policy(nn.Module):
             dtype = torch.get_autocast_dtype('cuda')
         flat = obs_u8.reshape(obs_u8.shape[0], -1)
         if flat.dtype == torch.uint8 and flat.is_cuda and dtype == torch.bfloat16 and not torch.is_grad_enabled() \
-                and flat.shape[1] == OBS:
-            # layer 1 straight from uint8 (HIP MFMA kernel); layer 2 with bias + ReLU in the hipBLASLt epilogue
-            h = trunk1(flat, self.l1.weight.to(dtype), self.l1.bias.to(dtype))
-            h = torch._addmm_activation(self.l2.bias.to(dtype), h, self.l2.weight.to(dtype).t())
-            out = self.head(h.to(self.head.weight.dtype)).float()
-            return out[:, :self.n_actions], out[:, self.n_actions]
+                and flat.shape[1] == OBS and self.l1.out_features == 256 and self.n_actions == N_ACTIONS:
+            return policy_fwd(flat, *self.packed(dtype))
         x = widen(flat, dtype)
         if x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_grad_enabled():
             # bias + ReLU in the hipBLASLt epilogue
@@ -53,19 +50,48 @@ class Policy(nn.Module):
         out = self.head(h).float()
         return out[:, :self.n_actions], out[:, self.n_actions]
 
+    def packed(self, dtype=torch.bfloat16, refresh=False):
+        """(packed bf16 weights, b1, b2, b3) for d1_policy_fwd, rebuilt when a parameter's
+        storage or version counter changes (optimizer steps and copy_ bump it; writes through
+        .data do not: pass refresh=True after those)."""
+        params = (self.l1.weight, self.l2.weight, self.head.weight, self.l1.bias, self.l2.bias, self.head.bias)
+        key = (dtype,) + tuple((q.data_ptr(), q._version) for q in params)
+        if refresh or getattr(self, '_packed_key', None) != key:
+            w1, w2, w3, b1, b2, b3 = (q.detach().to(dtype).contiguous() for q in params)
+            self._packed_val = (pack_weights(w1, w2, w3), b1, b2, b3)
+            self._packed_key = key
+        return self._packed_val
 
-def trunk1(obs_u8, w1, b1):
-    """relu(obs @ w1^T + b1) for uint8 obs [B, 1800] and bf16 w1 [256, 1800], b1 [256] on the
-    GPU: one HIP MFMA kernel, fp32 accumulation, bf16 [B, 256] out."""
-    obs_u8 = obs_u8.contiguous()
-    w1, b1 = w1.contiguous(), b1.contiguous()
-    assert obs_u8.dtype == torch.uint8 and w1.dtype == b1.dtype == torch.bfloat16
-    assert w1.shape == (256, OBS) and b1.shape == (256,) and obs_u8.shape[1] == OBS
-    h = torch.empty((obs_u8.shape[0], 256), dtype=torch.bfloat16, device=obs_u8.device)
+
+def pack_weights(w1, w2, w3):
+    """bf16 w1 [256, 1800], w2 [256, 256], w3 [17, 256] -> the operand-ordered buffer that
+    d1_policy_fwd reads (d1_policy_pack)."""
+    for w, shape in ((w1, (256, OBS)), (w2, (256, 256)), (w3, (N_ACTIONS + 1, 256))):
+        if w.dtype != torch.bfloat16 or tuple(w.shape) != shape or not w.is_contiguous() or not w.is_cuda:
+            raise ValueError(f'expected a contiguous CUDA bf16 tensor of shape {shape}')
     L = _lib.load()
-    _lib.check(L.d1_trunk1(obs_u8.data_ptr(), obs_u8.shape[0], w1.data_ptr(), b1.data_ptr(), h.data_ptr(),
-                           torch.cuda.current_stream(obs_u8.device).cuda_stream), 'd1_trunk1')
-    return h
+    wpk = torch.empty(L.d1_policy_packed_elems(), dtype=torch.bfloat16, device=w1.device)
+    _lib.check(L.d1_policy_pack(w1.data_ptr(), w2.data_ptr(), w3.data_ptr(), wpk.data_ptr(),
+                                torch.cuda.current_stream(w1.device).cuda_stream), 'd1_policy_pack')
+    return wpk
+
+
+def policy_fwd(obs_u8, wpk, b1, b2, b3, logits=None, value=None):
+    """The fused bf16 policy forward on uint8 obs [B, 1800]: (fp32 logits [B, 16], fp32 value [B])."""
+    obs_u8 = obs_u8.contiguous()
+    n = obs_u8.shape[0]
+    assert obs_u8.dtype == torch.uint8 and obs_u8.shape[1] == OBS
+    for b, size in ((b1, 256), (b2, 256), (b3, N_ACTIONS + 1)):
+        assert b.dtype == torch.bfloat16 and b.shape == (size,) and b.is_contiguous()
+    if logits is None:
+        logits = torch.empty((n, N_ACTIONS), dtype=torch.float32, device=obs_u8.device)
+    if value is None:
+        value = torch.empty(n, dtype=torch.float32, device=obs_u8.device)
+    L = _lib.load()
+    _lib.check(L.d1_policy_fwd(obs_u8.data_ptr(), n, wpk.data_ptr(), b1.data_ptr(), b2.data_ptr(), b3.data_ptr(),
+                               logits.data_ptr(), value.data_ptr(),
+                               torch.cuda.current_stream(obs_u8.device).cuda_stream), 'd1_policy_fwd')
+    return logits, value
 
 
 def widen(obs_u8, dtype):

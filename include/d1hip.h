@@ -153,12 +153,20 @@ int d1_sample_ar(const float *verb_logits, int nv, int ldv, const float *target_
                  uint64_t seed, uint32_t t, int32_t *verb, int32_t *target, int64_t *action, float *logp,
                  void *stream);
 
-/* The trunk's first layer as one MFMA kernel: h1 = relu(obs @ w1^T + b1) with obs
- * uint8 [M, 1800] (8-byte aligned), w1 bf16 [256, 1800] (torch Linear layout, 16-byte
- * aligned), b1 bf16 [256], fp32 accumulation, h1 bf16 [M, 256] (round to nearest even).
- * Replaces the widening pass + library GEMM of the policy forward
- * (gpu-d1/scripts/run_ring_ablations.py:209-223, BASELINE 1800->256 ReLU layer). */
-int d1_trunk1(const uint8_t *obs, int M, const void *w1, const void *b1, void *h1, void *stream);
+/* Rollout policy forward as one MFMA kernel: logits, value = head(relu(relu(obs W1^T + b1)
+ * W2^T + b2)) for obs uint8 [M, 1800] (8-byte aligned), hidden 256, a 17-row head (16
+ * logits + value); bf16 weights and biases in the torch Linear layout, fp32 accumulation,
+ * each layer's output rounded to bf16 (round to nearest even) as the bf16 torch forward
+ * rounds it, then logits fp32 [M, 16] (16-byte aligned) and value fp32 [M].
+ * Replaces the bf16 rollout forward of the policy (gpu-d1/scripts/run_ring_ablations.py:
+ * 209-223 at BASELINE's 1800 -> 256 -> 256 ReLU shape): widening, three GEMMs, dtype copy.
+ * The weights are first packed into operand order, once per weight update:
+ * d1_policy_pack(w1 [256,1800], w2 [256,256], w3 [17,256], wpk) with wpk holding
+ * d1_policy_packed_elems() bf16 values (16-byte aligned). */
+int64_t d1_policy_packed_elems(void);
+int d1_policy_pack(const void *w1, const void *w2, const void *w3, void *wpk, void *stream);
+int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
+                  float *logits, float *value, void *stream);
 
 /* Widen `count` uint8 observation bytes to bf16 (exact), for the policy trunk.
  * count must be a multiple of 16 and both pointers 16-byte aligned. */

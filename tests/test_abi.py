@@ -18,7 +18,8 @@ def test_header_declares_the_abi():
                                          'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_gae',
                                          'd1_obs_to_bf16', 'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step',
                                          'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
-                                         'd1_sample_ar', 'd1_los_table', 'd1_trunk1'])
+                                         'd1_sample_ar', 'd1_los_table', 'd1_policy_packed_elems',
+                                         'd1_policy_pack', 'd1_policy_fwd'])
     # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
     assert declared_symbols('d1learn.h', 'learn_') == sorted(
         ['learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size', 'learn_action_size',
@@ -113,3 +114,20 @@ def test_ppo_step_validation_without_gpu(pkg):
     assert L.d1_ppo_step(C.byref(s), None) == -1                  # fewer samples than one minibatch
     s = _lib.D1PPOStep(mb=1024, n=4096)
     assert L.d1_ppo_step(C.byref(s), None) == -1                  # null buffers
+
+
+def test_policy_fwd_validation_without_gpu(pkg):
+    """Packed-weight sizing and rejected forward arguments need no GPU."""
+    import importlib
+    _lib = importlib.import_module('dcss-auto_amd._lib')
+    L = _lib.load()
+    # W1 [8][29 chunks][4][64][8] + W2 [8][16][64][8] + head [16][64][8]
+    assert L.d1_policy_packed_elems() == 8 * 29 * 4 * 512 + 8 * 16 * 512 + 16 * 512
+    assert L.d1_policy_pack(None, None, None, None, None) == -1
+    assert L.d1_policy_fwd(None, 0, None, None, None, None, None, None, None) == 0      # empty batch
+    assert L.d1_policy_fwd(None, -1, None, None, None, None, None, None, None) == -1
+    assert L.d1_policy_fwd(None, 4, None, None, None, None, None, None, None) == -1     # null buffers
+    fake = 1 << 20
+    assert L.d1_policy_fwd(fake + 4, 4, fake, fake, fake, fake, fake, fake, None) == -1   # obs not 8-byte aligned
+    assert L.d1_policy_fwd(fake, 4, fake + 8, fake, fake, fake, fake, fake, None) == -1   # packed weights not 16-byte aligned
+    assert L.d1_policy_fwd(fake, 4, fake, fake, fake, fake, fake + 4, fake, None) == -1   # logits not 16-byte aligned

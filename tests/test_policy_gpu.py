@@ -132,21 +132,71 @@ def reference_loss(logits, values, actions, old_logp, adv, ret, clip=0.2):
     return pg + .25 * (values - ret).square().mean() - 0.01 * dist.entropy().mean()
 
 
-@pytest.mark.parametrize('M', [1, 1000, 4096])
-def test_trunk1_matches_fp32_reference(M):
-    """The fused uint8 -> MFMA first layer vs relu(obs @ W1^T + b1) in fp32: within bf16
-    rounding of the output (2e-2 relative to the output scale), and vs torch's own bf16 GEMM."""
+def _fwd_reference(obs, w1, b1, w2, b2, w3, b3, round_hidden=True):
+    """fp32 restatement of the bf16 forward: fp32 products and sums, each layer's output
+    rounded to bf16 where the bf16 torch forward rounds it (round_hidden=False: pure fp32)."""
+    r = (lambda x: x.to(torch.bfloat16).float()) if round_hidden else (lambda x: x)
+    h = r(torch.relu(obs.float() @ w1.float().T + b1.float()))
+    h = r(torch.relu(h @ w2.float().T + b2.float()))
+    return r(h @ w3.float().T + b3.float())
+
+
+@pytest.mark.parametrize('M', [1, 255, 1000, 4096 + 37])
+def test_policy_fwd_matches_fp32_reference(M):
+    """The fused uint8 -> MFMA forward (three layers, one launch) vs the fp32 restatement
+    with random weights AND biases of a scale where a misplaced bias, a permuted hidden unit
+    or a transposed weight moves the output by far more than the tolerance: within 2e-2 of
+    the output scale against pure fp32, and within 1e-2 against the restatement that
+    rounds h1/h2/out to bf16 like the kernel; also against torch's own bf16 GEMM chain."""
     P = importlib.import_module('dcss-auto_amd.policy')
-    torch.manual_seed(M)
-    obs = torch.randint(0, 60, (M, 1800), dtype=torch.uint8, device='cuda')
-    w1 = (torch.randn(256, 1800, device='cuda') * 0.02).to(torch.bfloat16)
-    b1 = (torch.randn(256, device='cuda') * 0.1).to(torch.bfloat16)
-    h = P.trunk1(obs, w1, b1)
-    ref = torch.relu(obs.float() @ w1.float().T + b1.float())
-    scale = ref.abs().max().clamp_min(1e-3)
-    assert ((h.float() - ref).abs().max() / scale).item() < 2e-2
-    bf = torch.relu(torch.addmm(b1, obs.to(torch.bfloat16), w1.T))
-    assert ((h.float() - bf.float()).abs().max() / scale).item() < 2e-2
+    print(f'[policy_fwd] M={M}', flush=True)
+    g = torch.Generator().manual_seed(M)
+    obs = torch.randint(0, 60, (M, 1800), dtype=torch.uint8, generator=g).cuda()
+    w1 = (torch.randn(256, 1800, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    b1 = (torch.randn(256, generator=g) * 5).to(torch.bfloat16).cuda()
+    w2 = (torch.randn(256, 256, generator=g) * 0.1).to(torch.bfloat16).cuda()
+    b2 = (torch.randn(256, generator=g) * 5).to(torch.bfloat16).cuda()
+    w3 = (torch.randn(17, 256, generator=g) * 0.1).to(torch.bfloat16).cuda()
+    b3 = (torch.randn(17, generator=g) * 5).to(torch.bfloat16).cuda()
+    wpk = P.pack_weights(w1, w2, w3)
+    logits, value = P.policy_fwd(obs, wpk, b1, b2, b3)
+    out = torch.cat([logits, value[:, None]], 1)
+    exact = _fwd_reference(obs, w1, b1, w2, b2, w3, b3, round_hidden=False)
+    scale = exact.abs().max().clamp_min(1e-3)
+    assert ((out - exact).abs().max() / scale).item() < 2e-2
+    emul = _fwd_reference(obs, w1, b1, w2, b2, w3, b3)
+    assert ((out - emul).abs().max() / scale).item() < 1e-2
+    with torch.no_grad():
+        h = torch.relu(torch.addmm(b1, obs.to(torch.bfloat16), w1.T))
+        h = torch.relu(torch.addmm(b2, h, w2.T))
+        tb = torch.addmm(b3, h, w3.T).float()
+    assert ((out - tb).abs().max() / scale).item() < 2e-2
+    # a different batch size sees the same per-sample outputs (no cross-sample leakage)
+    if M > 1:
+        l2_, v2_ = P.policy_fwd(obs[: M // 2], wpk, b1, b2, b3)
+        assert torch.equal(l2_, logits[: M // 2]) and torch.equal(v2_, value[: M // 2])
+
+
+def test_policy_module_uses_fused_forward_and_repacks():
+    """Policy.forward (bf16, no grad, uint8) runs the fused kernel, and a weight update
+    through copy_ is picked up by the packed-weight cache."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    model = P.Policy(seed=4).cuda().to(torch.bfloat16)
+    obs = torch.randint(0, 30, (777, 15, 15, 8), dtype=torch.uint8, device='cuda')
+    with torch.no_grad():
+        logits, value = model(obs)
+        wpk = model.packed()[0]
+        ref = _fwd_reference(obs.reshape(777, -1), model.l1.weight, model.l1.bias, model.l2.weight, model.l2.bias,
+                             model.head.weight, model.head.bias)
+        scale = ref.abs().max().clamp_min(1e-3)
+        assert ((torch.cat([logits, value[:, None]], 1) - ref).abs().max() / scale).item() < 1e-2
+        model.l2.bias.copy_(torch.randn(256, device='cuda').to(torch.bfloat16))
+        logits2, value2 = model(obs)
+        assert model.packed()[0] is not wpk
+        ref = _fwd_reference(obs.reshape(777, -1), model.l1.weight, model.l1.bias, model.l2.weight, model.l2.bias,
+                             model.head.weight, model.head.bias)
+        scale = ref.abs().max().clamp_min(1e-3)
+        assert ((torch.cat([logits2, value2[:, None]], 1) - ref).abs().max() / scale).item() < 1e-2
 
 
 def test_ppo_loss_matches_reference_fp32():
