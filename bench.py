@@ -141,7 +141,7 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
     pkg = importlib.import_module('dcss-auto_amd')
     P = importlib.import_module('dcss-auto_amd.policy')
     dev = torch.device('cuda:0')
-    env = pkg.Env(envs, pkg.stress_config(), seed=3)
+    env = pkg.Env(envs, pkg.stress_config(), seed=3, hash=False)
     model = P.ARPolicy(seed=0).to(dev).to(torch.bfloat16)
     actions = torch.zeros(envs, dtype=torch.int64, device=dev)
 
@@ -274,7 +274,7 @@ def main():
     dev = torch.device('cuda:0')
     cfg = pkg.baseline_config(args.monsters) if args.monsters <= 8 else pkg.stress_config()
     n = args.envs
-    env = pkg.Env(n, cfg, seed=1)
+    env = pkg.Env(n, cfg, seed=1, hash=False)
     model = policy_mod.Policy(seed=0).to(dev).to(torch.bfloat16)
     actions = torch.zeros(n, dtype=torch.int64, device=dev)
     logp = torch.zeros(n, dtype=torch.float32, device=dev)

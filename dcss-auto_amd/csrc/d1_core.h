@@ -24,10 +24,7 @@ struct Smem {
     uint32_t front[ROWS_WORDS];
     union {
         uint8_t dist[N];        // BFS layer mod 256, valid where `reach` is set (monster phase)
-        struct {
-            uint32_t win[225];  // observation window: kind+1 | hp<<8 | stair<<16 (observation)
-            int32_t rowpre[72]; // inclusive per-row prefix counts (episode reset)
-        };
+        int32_t rowpre[72];     // inclusive per-row prefix counts (episode reset)
     };
 };
 

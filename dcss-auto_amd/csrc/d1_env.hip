@@ -226,53 +226,68 @@ __device__ __forceinline__ void transition(Ctx &x, int action, float *out, const
 // 6 remembered stair, 7 frontier anchor (seen floor with an in-bounds unviewed
 // neighbour; the FRONTIER_RING_MEMORY_WALLS rule of
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:269-280).
+//
+// Lanes 0..14 build their window row (dy = lane - 7) as 15-bit strips (bit k = column
+// px - 7 + k): wall | viewed-floor << 16 in w0, visible | frontier << 16 in w1. A cell lane
+// then fetches its row's two words with one shuffle each and assembles its 8 bytes from
+// single bits; monsters and stairs in the window are applied by uniform loops. No LDS
+// writes and no barriers.
+__device__ __forceinline__ uint32_t row_strip15(Row r, int px) {   // bits px-7 .. px+7, zero outside 0..95
+    const int s = px - 7, k = s >> 5;                               // s >= -7, so k in -1..2
+    const uint32_t w0 = k == 0 ? r.a : k == 1 ? r.b : k == 2 ? r.c : 0u;
+    const uint32_t w1 = k == -1 ? r.a : k == 0 ? r.b : k == 1 ? r.c : 0u;
+    return __builtin_amdgcn_alignbit(w1, w0, (uint32_t)s & 31u) & 0x7FFFu;
+}
 __device__ __forceinline__ void write_obs(Ctx &x, uint8_t *o) {
     Smem *sm = x.sm;
-    int px = x.player % W, py = x.player / W;
-    // frontier rows of the window into sm->front
+    const int px = x.player % W, py = x.player / W;
+    uint32_t w0 = 0x7FFFu, w1 = 0;   // rows outside the map: all wall
     {
-        int y = py + x.lane - 7;
+        const int dy = x.lane - 7, y = py + dy;
         if (x.lane < 15 && y >= 0 && y < H) {
             const Row all = row_range(0, W - 1);
             Row u{0, 0, 0};
             for (int yy = y - 1; yy <= y + 1; yy++)
                 if (yy >= 0 && yy < H) u = row_or(u, row_andn(all, row_ld(sm->viewed, yy)));
             u = row_and(row_or(u, row_or(row_shl1(u), row_shr1(u))), all);
-            Row f = row_and(row_and(row_ld(sm->floor, y), row_ld(sm->viewed, y)), u);
-            row_st(sm->front, y, f);
+            const Row vw = row_ld(sm->viewed, y), fl = row_ld(sm->floor, y);
+            const int klo = imax(0, 7 - px), khi = imin(14, W + 6 - px);
+            const uint32_t ib = ((2u << khi) - 1u) & ~((1u << klo) - 1u);
+            const uint32_t v = row_strip15(vw, px), f = row_strip15(fl, px);
+            const uint32_t fr = row_strip15(row_and(row_and(fl, vw), u), px) & ib;
+            const int ay = iabs(dy);
+            uint32_t R = 0, L = 0;
+            if (dy >= 0) { R |= (uint32_t)(x.vis0 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis1 >> (8 * ay)) & 0xFFu; }
+            if (dy <= 0) { R |= (uint32_t)(x.vis3 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis2 >> (8 * ay)) & 0xFFu; }
+            const uint32_t vis = ((__builtin_bitreverse32(L) >> 24) | (R << 7)) & ib;
+            w0 = ((~ib | (v & ~f)) & 0x7FFFu) | ((v & f & ib) << 16);
+            w1 = vis | (fr << 16);
         }
     }
-    for (int cidx = x.lane; cidx < 225; cidx += 64) sm->win[cidx] = 0;
-    __syncthreads();
-    if (x.lane < x.c->count && x.mhp > 0) {
-        int dx = x.mpos % W - px, dy = x.mpos / W - py;
-        if (iabs(dx) <= 7 && iabs(dy) <= 7)
-            sm->win[(dy + 7) * 15 + dx + 7] = (uint32_t)(x.mkind + 1) | ((uint32_t)imin(x.mhp, 255) << 8);
-    }
-    __syncthreads();
+    // living monsters and known stairs inside the window (uniform)
+    uint64_t mon = ballot(x.lane < x.c->count && x.mhp > 0 && iabs(x.mpos % W - px) <= 7 && iabs(x.mpos / W - py) <= 7);
+    const uint32_t php = (uint32_t)imin(imax(x.hp, 0), 255);
+    int sc[3];
     for (int k = 0; k < 3; k++) {
-        int sp = stair_at(x, k);
-        if (x.lane == 0 && sp >= 0) {
-            int dx = sp % W - px, dy = sp / W - py;
-            if (iabs(dx) <= 7 && iabs(dy) <= 7) sm->win[(dy + 7) * 15 + dx + 7] |= 1u << 16;
-        }
+        const int sp = stair_at(x, k), dx = sp % W - px, dy = sp / W - py;
+        sc[k] = sp >= 0 && iabs(dx) <= 7 && iabs(dy) <= 7 ? (dy + 7) * 15 + dx + 7 : -1;
     }
-    __syncthreads();
-    uint32_t php = (uint32_t)imin(imax(x.hp, 0), 255);
-    for (int cidx = x.lane; cidx < 225; cidx += 64) {
-        int dy = cidx / 15 - 7, dx = cidx % 15 - 7, xx = px + dx, yy = py + dy;
-        uint32_t lo = 0, hi = php << 8;   // bytes 4..7 = ch4 hp, ch5 player hp, ch6 stair, ch7 frontier
-        if (!inb(xx, yy)) lo = 1;
-        else {
-            bool vw = bit_at(sm->viewed, xx, yy), fl = bit_at(sm->floor, xx, yy);
-            bool vis = vis_rel(x, dx, dy);
-            uint32_t wv = sm->win[cidx];
-            lo = (uint32_t)(vw && !fl) | ((uint32_t)(vw && fl) << 8) | ((uint32_t)vis << 16);
-            if (vis && (wv & 0xFFu)) { lo |= (wv & 0xFFu) << 24; hi |= (wv >> 8) & 0xFFu; }
-            if ((wv >> 16) & 1u && vw && fl) hi |= 1u << 16;
-            if (bit_at(sm->front, xx, yy)) hi |= 1u << 24;
+    for (int c0 = 0; c0 < 225; c0 += 64) {
+        const int cidx = c0 + x.lane, r = cidx / 15, k = cidx - 15 * r;
+        const uint32_t a = (uint32_t)__shfl((int)w0, imin(r, 14)) >> k, b = (uint32_t)__shfl((int)w1, imin(r, 14)) >> k;
+        uint32_t lo = (a & 1u) | ((a >> 16) & 1u) << 8 | (b & 1u) << 16;
+        uint32_t hi = php << 8 | ((b >> 16) & 1u) << 24;
+        for (uint64_t m = mon; m; m &= m - 1) {
+            const int i = __ffsll((unsigned long long)m) - 1, mp = lane_val(x.mpos, i);
+            const int mc = (mp / W - py + 7) * 15 + mp % W - px + 7;
+            if (cidx == mc && (b & 1u)) {
+                lo |= (uint32_t)(lane_val(x.mkind, i) + 1) << 24;
+                hi |= (uint32_t)imin(lane_val(x.mhp, i), 255);
+            }
         }
-        *(uint2 *)(o + cidx * 8) = make_uint2(lo, hi);
+        for (int s = 0; s < 3; s++)
+            if (cidx == sc[s] && ((a >> 16) & 1u)) hi |= 1u << 16;
+        if (cidx < 225) *(uint2 *)(o + cidx * 8) = make_uint2(lo, hi);
     }
 }
 // Sum over canonical words of fmix32(word ^ index*0x9E3779B9) (index map in
@@ -427,8 +442,10 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
     reset(x, cg);
     store_world(x, row, max_m);
     if (obs) write_obs(x, obs + (size_t)env * D1_OBS_BYTES);
-    uint32_t h = state_hash(x);
-    if (hash && x.lane == 0) hash[env] = h;
+    if (hash) {   // the digest costs about a tenth of a step: callers that do not ask skip it
+        const uint32_t h = state_hash(x);
+        if (x.lane == 0) hash[env] = h;
+    }
 }
 
 __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg,
@@ -455,8 +472,10 @@ __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, s
         o4[1] = make_float4(o8[4], o8[5], o8[6], o8[7]);
     }
     if (obs) write_obs(x, obs + (size_t)env * D1_OBS_BYTES);
-    uint32_t h = state_hash(x);
-    if (hash && x.lane == 0) hash[env] = h;
+    if (hash) {   // the digest costs about a tenth of a step: callers that do not ask skip it
+        const uint32_t h = state_hash(x);
+        if (x.lane == 0) hash[env] = h;
+    }
 }
 
 // ---------------------------------------------------------------- monster-wait workload

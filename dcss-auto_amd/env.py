@@ -6,7 +6,8 @@ Same surface: ``Env(batch, ..., seed, device)``, ``reset(seed) -> obs``,
 ``out[:, 1]`` done, and the ``state/obs/out`` tensors as attributes. Calls run
 asynchronously on PyTorch's current stream, as the reference's do
 (gpu-d1/scripts/learn_env.py:83-85). Observations are uint8 [batch, 15, 15, 8];
-``hash`` holds the per-env 32-bit state hash after every call.
+``hash`` holds the per-env 32-bit state hash after every call (a parity digest the
+reference does not have; ``Env(..., hash=False)`` skips it in step()).
 """
 import ctypes as C
 
@@ -17,7 +18,8 @@ from . import _lib, config as cfgmod, data
 
 
 class Env:
-    def __init__(self, batch=512, cfg=None, seed=0, device='cuda', max_monsters=None):
+    def __init__(self, batch=512, cfg=None, seed=0, device='cuda', max_monsters=None, hash=True):
+        self.with_hash = hash
         self.device = torch.device('cuda:0' if device == 'cuda' else device)
         if self.device.type != 'cuda':
             raise ValueError('the HIP environment runs on a GPU device; the CPU restatement is test-only')
@@ -72,5 +74,6 @@ class Env:
             dst = obs
         _lib.check(self.lib.d1_step(self.state.data_ptr(), self.batch, self.max_monsters, C.byref(self.cfg),
                                     C.byref(self.tables), actions.data_ptr(), dst.data_ptr(),
-                                    self.out.data_ptr(), self.hash.data_ptr(), act, self.stream), 'd1_step')
+                                    self.out.data_ptr(), self.hash.data_ptr() if self.with_hash else None, act,
+                                    self.stream), 'd1_step')
         return dst, self.out

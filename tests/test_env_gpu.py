@@ -60,3 +60,21 @@ def test_hip_matches_oracle(pkg, name, spec, batch, steps, nact):
         dones += int(cpu.out[:, 1].sum())
     assert dones > 0
     print(f'[parity] {name} ok, {dones} episode ends', flush=True)
+
+
+def test_step_without_hash_is_the_same_step(pkg):
+    """Env(hash=False) passes no hash buffer: the digest is skipped, the state, the
+    observation and out[] are the same as with it, and the hash tensor keeps its value."""
+    print('[parity] hash off', flush=True)
+    cfg = pkg.baseline_config(8)
+    a = pkg.Env(300, cfg, seed=5)
+    b = pkg.Env(300, cfg, seed=5, hash=False)
+    h0 = b.hash.clone()
+    g = torch.Generator().manual_seed(9)
+    for _ in range(60):
+        act = torch.randint(0, 16, (300,), generator=g).cuda()
+        a.step(act)
+        b.step(act)
+    torch.cuda.synchronize()
+    assert torch.equal(a.state, b.state) and torch.equal(a.obs, b.obs) and torch.equal(a.out, b.out)
+    assert torch.equal(b.hash, h0)
