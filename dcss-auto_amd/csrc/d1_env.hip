@@ -311,28 +311,6 @@ __device__ __forceinline__ uint32_t state_hash(Ctx &x) {
 }
 
 // ---------------------------------------------------------------- load / store
-__device__ __forceinline__ void load_world(Ctx &x, const uint8_t *row, int max_m) {
-    Hdr h = *(const Hdr *)row;
-    x.player = h.player; x.hp = h.hp; x.regen = h.regen; x.ncells = h.ncells;
-    x.ticks = h.ticks; x.killed = h.killed; x.decisions = h.decisions; x.floor_seen = h.floor_seen;
-    x.episode = h.episode; x.first_stair_tick = h.first_stair_tick;
-    x.stairs = pack_stairs(h.stairs[0], h.stairs[1], h.stairs[2]);
-    x.blocks = h.blocks; x.t = h.t; x.env_id = h.env_id;
-    if (x.c->rng_mode == 0) x.g.pcg_load(h.rng_state, h.rng_inc);
-    else x.g.counter(h.rng_state, h.env_id, h.t, 0);
-    Mon m{-1, 0, -30000, 0, 0};
-    if (x.lane < max_m) m = ((const Mon *)(row + OFF_MON))[x.lane];
-    const uint64_t *vw = (const uint64_t *)(row + OFF_VIEW);
-    x.vis0 = vw[0]; x.vis1 = vw[1]; x.vis2 = vw[2]; x.vis3 = vw[3];
-    x.mpos = m.pos; x.mhp = m.hp; x.menergy = m.energy; x.mawake = m.awake; x.mkind = m.kind;
-    const uint32_t *vg = (const uint32_t *)(row + off_viewed(max_m));
-    const uint32_t *fg = (const uint32_t *)(row + off_floor(max_m));
-    for (int w = x.lane; w < ROWS_WORDS; w += 64) { x.sm->viewed[w] = vg[w]; x.sm->floor[w] = fg[w]; x.sm->occ[w] = 0; }
-    __syncthreads();
-    if (x.lane < x.c->count && x.mhp > 0)
-        atomicOr(&x.sm->occ[(x.mpos / W) * RW + ((x.mpos % W) >> 5)], 1u << ((x.mpos % W) & 31));
-    __syncthreads();
-}
 __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
     if (x.lane == 0) {
         Hdr h;
@@ -404,6 +382,65 @@ __device__ __forceinline__ void generate_level(Ctx &x, uint64_t seed, uint32_t e
     }
 }
 
+// ---------------------------------------------------------------- prefetched load
+// A k_step workgroup runs several consecutive worlds; the next world's row is fetched into
+// registers while the current one steps, so its HBM latency is off the critical path.
+// Lane l holds dword l of header + view (l < 24), its monster (l < max_m) and words
+// l + 64i of the viewed and floor rows; every lane holds the action and the active flag.
+// Addresses are clamped in bounds (the lanes past a field read a copy of its last element).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));   // register-resident 8-byte piece
+struct Pre {
+    uint32_t hv;
+    u32x2 mon;
+    uint32_t vw[4], fl[4];
+    int64_t act;
+    int on;
+};
+__device__ __forceinline__ void prefetch_world(Pre &pf, const uint8_t *row, int max_m, const int64_t *actions,
+                                               const uint8_t *active, int env, int lane) {
+    pf.hv = ((const uint32_t *)row)[imin(lane, 23)];
+    pf.mon = ((const u32x2 *)(row + OFF_MON))[imin(lane, max_m - 1)];
+    const uint32_t *vg = (const uint32_t *)(row + off_viewed(max_m)), *fg = (const uint32_t *)(row + off_floor(max_m));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int w = imin(lane + 64 * i, ROWS_WORDS - 1);
+        pf.vw[i] = vg[w];
+        pf.fl[i] = fg[w];
+    }
+    pf.act = actions[env];
+    pf.on = active ? active[env] : 1;
+}
+// load_world from the prefetched registers
+__device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
+    auto hw = [&](int k) { return (uint32_t)__builtin_amdgcn_readlane((int)pf.hv, k); };
+    x.env_id = hw(4); x.t = hw(5); x.episode = (int)hw(6);
+    x.player = (int16_t)(hw(7) & 0xFFFFu); x.hp = (int16_t)(hw(7) >> 16);
+    x.regen = (int16_t)(hw(8) & 0xFFFFu); x.ncells = (int16_t)(hw(8) >> 16);
+    x.ticks = (int)hw(9); x.killed = (int)hw(10); x.decisions = (int)hw(11); x.floor_seen = (int)hw(12);
+    x.stairs = pack_stairs((int16_t)(hw(13) & 0xFFFFu), (int16_t)(hw(13) >> 16), (int16_t)(hw(14) & 0xFFFFu));
+    x.blocks = (int16_t)(hw(14) >> 16); x.first_stair_tick = (int)hw(15);
+    const uint64_t rs = (uint64_t)hw(1) << 32 | hw(0), ri = (uint64_t)hw(3) << 32 | hw(2);
+    if (x.c->rng_mode == 0) x.g.pcg_load(rs, ri);
+    else x.g.counter(rs, x.env_id, x.t, 0);
+    x.vis0 = (uint64_t)hw(17) << 32 | hw(16); x.vis1 = (uint64_t)hw(19) << 32 | hw(18);
+    x.vis2 = (uint64_t)hw(21) << 32 | hw(20); x.vis3 = (uint64_t)hw(23) << 32 | hw(22);
+    if (x.lane < max_m) {
+        x.mpos = (int16_t)(pf.mon.x & 0xFFFFu); x.mhp = (int16_t)(pf.mon.x >> 16);
+        x.menergy = (int16_t)(pf.mon.y & 0xFFFFu); x.mawake = (pf.mon.y >> 16) & 0xFFu; x.mkind = pf.mon.y >> 24;
+    } else {
+        x.mpos = -1; x.mhp = 0; x.menergy = -30000; x.mawake = 0; x.mkind = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int w = x.lane + 64 * i;
+        if (w < ROWS_WORDS) { x.sm->viewed[w] = pf.vw[i]; x.sm->floor[w] = pf.fl[i]; x.sm->occ[w] = 0; }
+    }
+    __syncthreads();
+    if (x.lane < x.c->count && x.mhp > 0)
+        atomicOr(&x.sm->occ[(x.mpos / W) * RW + ((x.mpos % W) >> 5)], 1u << ((x.mpos % W) & 31));
+    __syncthreads();
+}
+
 // ---------------------------------------------------------------- kernels
 __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg,
                                              D1Tables tab, uint64_t seed, uint8_t *obs, uint32_t *hash) {
@@ -448,33 +485,50 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
     }
 }
 
+// Worlds per k_step workgroup: world blockIdx.x * STEP_WPB + k, k = 0..STEP_WPB-1.
+constexpr int STEP_WPB = 2;
 __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg,
                                              D1Tables tab, const int64_t *actions, uint8_t *obs, float *out,
                                              uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
-    int env = blockIdx.x;
-    if (env >= n) return;
-    if (active && !active[env]) return;
-    uint8_t *row = state + (size_t)env * row_bytes;
+    const int first = blockIdx.x * STEP_WPB, last = imin(n, first + STEP_WPB);
     Ctx x;
     x.sm = &sm; x.c = &cfg; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
-    load_world(x, row, max_m);
-    const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
-    int64_t a = actions[env];
-    int action = a < 0 || a > 1000 ? -1 : (int)a;
-    float o8[8];
-    transition(x, action, o8, cg);
-    x.t++;
-    store_world(x, row, max_m);
-    if (out && x.lane == 0) {
-        float4 *o4 = (float4 *)(out + (size_t)env * D1_OUT);
-        o4[0] = make_float4(o8[0], o8[1], o8[2], o8[3]);
-        o4[1] = make_float4(o8[4], o8[5], o8[6], o8[7]);
-    }
-    if (obs) write_obs(x, obs + (size_t)env * D1_OBS_BYTES);
-    if (hash) {   // the digest costs about a tenth of a step: callers that do not ask skip it
-        const uint32_t h = state_hash(x);
-        if (x.lane == 0) hash[env] = h;
+    Pre pf;
+    prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
+    for (int env = first; env < last; env++) {
+        // Opaque per world: otherwise every lane-derived constant of the world step is
+        // hoisted out of this loop and kept live across it.
+        int lane = lane_id();
+        asm volatile("" : "+v"(lane));
+        x.lane = lane;
+        uint8_t *row = state + (size_t)env * row_bytes;
+        const int on = __builtin_amdgcn_readfirstlane(pf.on);
+        const int64_t a = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(pf.act >> 32)) << 32 |
+                                    (uint32_t)__builtin_amdgcn_readfirstlane((int)pf.act));
+        if (!on) {   // an inactive env keeps its state and all its output rows
+            if (env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
+            continue;
+        }
+        unpack_world(x, pf, max_m);
+        const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
+        const int action = a < 0 || a > 1000 ? -1 : (int)a;
+        float o8[8];
+        transition(x, action, o8, cg);
+        x.t++;
+        // the next world's loads overlap this world's stores, observation and digest
+        if (env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
+        store_world(x, row, max_m);
+        if (out && x.lane == 0) {
+            float4 *o4 = (float4 *)(out + (size_t)env * D1_OUT);
+            o4[0] = make_float4(o8[0], o8[1], o8[2], o8[3]);
+            o4[1] = make_float4(o8[4], o8[5], o8[6], o8[7]);
+        }
+        if (obs) write_obs(x, obs + (size_t)env * D1_OBS_BYTES);
+        if (hash) {   // the digest costs about a tenth of a step: callers that do not ask skip it
+            const uint32_t h = state_hash(x);
+            if (x.lane == 0) hash[env] = h;
+        }
     }
 }
 
@@ -730,7 +784,8 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
     if (e) return e;
     if (!state || !actions) return D1_E_ARG;
     if (n == 0) return 0;
-    hipLaunchKernelGGL(d1::k_step, dim3(n), dim3(64), 0, (hipStream_t)stream, (uint8_t *)state, n, max_monsters,
+    hipLaunchKernelGGL(d1::k_step, dim3((n + d1::STEP_WPB - 1) / d1::STEP_WPB), dim3(64), 0, (hipStream_t)stream,
+                       (uint8_t *)state, n, max_monsters,
                        (size_t)d1::state_bytes(max_monsters), *cfg, *tab, actions, obs, out, hash, active);
     return (int)hipGetLastError();
 }
