@@ -264,31 +264,48 @@ __device__ __forceinline__ void write_obs(Ctx &x, uint8_t *o) {
             w1 = vis | (fr << 16);
         }
     }
-    // living monsters and known stairs inside the window (uniform)
-    uint64_t mon = ballot(x.lane < x.c->count && x.mhp > 0 && iabs(x.mpos % W - px) <= 7 && iabs(x.mpos / W - py) <= 7);
+    // the four cell chunks of this lane (cell c0 + lane, c0 = 0, 64, 128, 192)
     const uint32_t php = (uint32_t)imin(imax(x.hp, 0), 255);
-    int sc[3];
+    uint32_t lo[4], hi[4], vis[4], vf[4];
+    int cell[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int cidx = 64 * c + x.lane, r = cidx / 15, k = cidx - 15 * r;
+        const uint32_t a = (uint32_t)__shfl((int)w0, imin(r, 14)) >> k, b = (uint32_t)__shfl((int)w1, imin(r, 14)) >> k;
+        cell[c] = cidx;
+        vis[c] = b & 1u;
+        vf[c] = (a >> 16) & 1u;
+        lo[c] = (a & 1u) | vf[c] << 8 | vis[c] << 16;
+        hi[c] = php << 8 | ((b >> 16) & 1u) << 24;
+    }
+    // living monsters inside the window: each monster lane computes its cell and bytes once,
+    // then the owner lane of that cell takes them when the cell is visible
+    int mc = -1;
+    if (x.lane < x.c->count && x.mhp > 0) {
+        const int dx = x.mpos % W - px, dy = x.mpos / W - py;
+        if (iabs(dx) <= 7 && iabs(dy) <= 7) mc = (dy + 7) * 15 + dx + 7;
+    }
+    const uint32_t mlo = (uint32_t)(x.mkind + 1) << 24, mhi = (uint32_t)imin(x.mhp, 255);
+    for (uint64_t m = ballot(mc >= 0); m; m &= m - 1) {
+        const int i = __ffsll((unsigned long long)m) - 1;
+        const int ci = lane_val(mc, i), c = ci >> 6;
+        const uint32_t ol = (uint32_t)lane_val((int)mlo, i), oh = (uint32_t)lane_val((int)mhi, i);
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++)
+            if (cc == c && cell[cc] == ci && vis[cc]) { lo[cc] |= ol; hi[cc] |= oh; }
+    }
+    // known stairs inside the window mark a viewed floor cell
     for (int k = 0; k < 3; k++) {
         const int sp = stair_at(x, k), dx = sp % W - px, dy = sp / W - py;
-        sc[k] = sp >= 0 && iabs(dx) <= 7 && iabs(dy) <= 7 ? (dy + 7) * 15 + dx + 7 : -1;
+        if (sp < 0 || iabs(dx) > 7 || iabs(dy) > 7) continue;
+        const int ci = (dy + 7) * 15 + dx + 7, c = ci >> 6;
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++)
+            if (cc == c && cell[cc] == ci && vf[cc]) hi[cc] |= 1u << 16;
     }
-    for (int c0 = 0; c0 < 225; c0 += 64) {
-        const int cidx = c0 + x.lane, r = cidx / 15, k = cidx - 15 * r;
-        const uint32_t a = (uint32_t)__shfl((int)w0, imin(r, 14)) >> k, b = (uint32_t)__shfl((int)w1, imin(r, 14)) >> k;
-        uint32_t lo = (a & 1u) | ((a >> 16) & 1u) << 8 | (b & 1u) << 16;
-        uint32_t hi = php << 8 | ((b >> 16) & 1u) << 24;
-        for (uint64_t m = mon; m; m &= m - 1) {
-            const int i = __ffsll((unsigned long long)m) - 1, mp = lane_val(x.mpos, i);
-            const int mc = (mp / W - py + 7) * 15 + mp % W - px + 7;
-            if (cidx == mc && (b & 1u)) {
-                lo |= (uint32_t)(lane_val(x.mkind, i) + 1) << 24;
-                hi |= (uint32_t)imin(lane_val(x.mhp, i), 255);
-            }
-        }
-        for (int s = 0; s < 3; s++)
-            if (cidx == sc[s] && ((a >> 16) & 1u)) hi |= 1u << 16;
-        if (cidx < 225) *(uint2 *)(o + cidx * 8) = make_uint2(lo, hi);
-    }
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        if (cell[c] < 225) *(uint2 *)(o + cell[c] * 8) = make_uint2(lo[c], hi[c]);
 }
 // Sum over canonical words of fmix32(word ^ index*0x9E3779B9) (index map in
 // include/d1hip.h's companion spec: scalars 0-14, monsters 100+2i, viewed 1000+3y+j).
@@ -410,7 +427,9 @@ __device__ __forceinline__ void prefetch_world(Pre &pf, const uint8_t *row, int 
     pf.act = actions[env];
     pf.on = active ? active[env] : 1;
 }
-// load_world from the prefetched registers
+// load_world from the prefetched registers; RM is the config's RNG mode (a compile-time
+// constant, so a kernel carries one generator's state and code)
+template <int RM>
 __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
     auto hw = [&](int k) { return (uint32_t)__builtin_amdgcn_readlane((int)pf.hv, k); };
     x.env_id = hw(4); x.t = hw(5); x.episode = (int)hw(6);
@@ -420,7 +439,7 @@ __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
     x.stairs = pack_stairs((int16_t)(hw(13) & 0xFFFFu), (int16_t)(hw(13) >> 16), (int16_t)(hw(14) & 0xFFFFu));
     x.blocks = (int16_t)(hw(14) >> 16); x.first_stair_tick = (int)hw(15);
     const uint64_t rs = (uint64_t)hw(1) << 32 | hw(0), ri = (uint64_t)hw(3) << 32 | hw(2);
-    if (x.c->rng_mode == 0) x.g.pcg_load(rs, ri);
+    if (RM == 0) x.g.pcg_load(rs, ri);
     else x.g.counter(rs, x.env_id, x.t, 0);
     x.vis0 = (uint64_t)hw(17) << 32 | hw(16); x.vis1 = (uint64_t)hw(19) << 32 | hw(18);
     x.vis2 = (uint64_t)hw(21) << 32 | hw(20); x.vis3 = (uint64_t)hw(23) << 32 | hw(22);
@@ -487,6 +506,7 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
 
 // Worlds per k_step workgroup: world blockIdx.x * STEP_WPB + k, k = 0..STEP_WPB-1.
 constexpr int STEP_WPB = 2;
+template <int RM>
 __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg,
                                              D1Tables tab, const int64_t *actions, uint8_t *obs, float *out,
                                              uint32_t *hash, const uint8_t *active) {
@@ -510,7 +530,7 @@ __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, s
             if (env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
             continue;
         }
-        unpack_world(x, pf, max_m);
+        unpack_world<RM>(x, pf, max_m);
         const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
         const int action = a < 0 || a > 1000 ? -1 : (int)a;
         float o8[8];
@@ -784,7 +804,8 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
     if (e) return e;
     if (!state || !actions) return D1_E_ARG;
     if (n == 0) return 0;
-    hipLaunchKernelGGL(d1::k_step, dim3((n + d1::STEP_WPB - 1) / d1::STEP_WPB), dim3(64), 0, (hipStream_t)stream,
+    auto kern = cfg->rng_mode == 0 ? d1::k_step<0> : d1::k_step<1>;
+    hipLaunchKernelGGL(kern, dim3((n + d1::STEP_WPB - 1) / d1::STEP_WPB), dim3(64), 0, (hipStream_t)stream,
                        (uint8_t *)state, n, max_monsters,
                        (size_t)d1::state_bytes(max_monsters), *cfg, *tab, actions, obs, out, hash, active);
     return (int)hipGetLastError();
