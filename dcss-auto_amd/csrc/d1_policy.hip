@@ -23,11 +23,10 @@ __device__ inline uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint
     return c0;
 }
 
-__global__ __launch_bounds__(256) void k_sample(const float *__restrict__ logits, int n, int k, int ld, uint32_t key0,
-                                                uint32_t key1, uint32_t t, int64_t *__restrict__ actions,
-                                                float *__restrict__ logp) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+// the sample of row i at counter step t (shared by the two entry points: identical results)
+__device__ __forceinline__ void sample_row(const float *__restrict__ logits, int i, int k, int ld, uint32_t key0,
+                                           uint32_t key1, uint32_t t, int64_t *__restrict__ actions,
+                                           float *__restrict__ logp) {
     const float *l = logits + (size_t)i * ld;
     float m = l[0];
     for (int j = 1; j < k; j++) m = fmaxf(m, l[j]);
@@ -43,6 +42,24 @@ __global__ __launch_bounds__(256) void k_sample(const float *__restrict__ logits
     }
     if (actions) actions[i] = a;
     if (logp) logp[i] = l[a] - m - logf(s);
+}
+
+__global__ __launch_bounds__(256) void k_sample(const float *__restrict__ logits, int n, int k, int ld, uint32_t key0,
+                                                uint32_t key1, uint32_t t, int64_t *__restrict__ actions,
+                                                float *__restrict__ logp) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    sample_row(logits, i, k, ld, key0, key1, t, actions, logp);
+}
+// the counter step read from device memory (*t_dev + t_add), so that a captured graph
+// samples a new step on every replay
+__global__ __launch_bounds__(256) void k_sample_dev(const float *__restrict__ logits, int n, int k, int ld,
+                                                    uint32_t key0, uint32_t key1, const uint32_t *__restrict__ t_dev,
+                                                    uint32_t t_add, int64_t *__restrict__ actions,
+                                                    float *__restrict__ logp) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    sample_row(logits, i, k, ld, key0, key1, *t_dev + t_add, actions, logp);
 }
 
 __global__ __launch_bounds__(256) void k_gae(const float *__restrict__ reward, const uint8_t *__restrict__ done,
@@ -152,6 +169,14 @@ int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t
     if (n == 0) return 0;
     hipLaunchKernelGGL(d1p::k_sample, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, logits, n, k, ld,
                        (uint32_t)seed, (uint32_t)(seed >> 32), t, actions, logp);
+    return (int)hipGetLastError();
+}
+int d1_sample_dev(const float *logits, int n, int k, int ld, uint64_t seed, const uint32_t *t_dev, uint32_t t_add,
+                  int64_t *actions, float *logp, void *stream) {
+    if (n < 0 || k < 1 || k > 64 || ld < k || (n && (!logits || !t_dev))) return D1_E_ARG;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(d1p::k_sample_dev, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, logits, n, k, ld,
+                       (uint32_t)seed, (uint32_t)(seed >> 32), t_dev, t_add, actions, logp);
     return (int)hipGetLastError();
 }
 int d1_sample_ar(const float *verb_logits, int nv, int ldv, const float *target_logits, int nt, int ldt, int n,

@@ -63,14 +63,16 @@ class Policy(nn.Module):
         return self._packed_val
 
 
-def pack_weights(w1, w2, w3):
+def pack_weights(w1, w2, w3, out=None):
     """bf16 w1 [256, 1800], w2 [256, 256], w3 [17, 256] -> the operand-ordered buffer that
-    d1_policy_fwd reads (d1_policy_pack)."""
+    d1_policy_fwd reads (d1_policy_pack); `out` repacks into an existing buffer."""
     for w, shape in ((w1, (256, OBS)), (w2, (256, 256)), (w3, (N_ACTIONS + 1, 256))):
         if w.dtype != torch.bfloat16 or tuple(w.shape) != shape or not w.is_contiguous() or not w.is_cuda:
             raise ValueError(f'expected a contiguous CUDA bf16 tensor of shape {shape}')
     L = _lib.load()
-    wpk = torch.empty(L.d1_policy_packed_elems(), dtype=torch.bfloat16, device=w1.device)
+    wpk = out if out is not None else torch.empty(L.d1_policy_packed_elems(), dtype=torch.bfloat16, device=w1.device)
+    if wpk.dtype != torch.bfloat16 or wpk.numel() != L.d1_policy_packed_elems() or not wpk.is_contiguous():
+        raise ValueError('the packed buffer must hold d1_policy_packed_elems() contiguous bf16 values')
     _lib.check(L.d1_policy_pack(w1.data_ptr(), w2.data_ptr(), w3.data_ptr(), wpk.data_ptr(),
                                 torch.cuda.current_stream(w1.device).cuda_stream), 'd1_policy_pack')
     return wpk
@@ -120,6 +122,21 @@ def sample(logits, seed, t, actions=None, logp=None):
     L = _lib.load()
     _lib.check(L.d1_sample(logits.data_ptr(), n, k, logits.stride(0), seed, t & 0xFFFFFFFF, actions.data_ptr(),
                            logp.data_ptr(), torch.cuda.current_stream(logits.device).cuda_stream), 'd1_sample')
+    return actions, logp
+
+
+def sample_dev(logits, seed, t_dev, t_add, actions, logp):
+    """sample() with the counter step read on the device: t = t_dev[0] + t_add (int32
+    tensor, read as uint32), so a captured graph draws a new step on every replay."""
+    if logits.dtype != torch.float32 or logits.stride(1) != 1:
+        raise ValueError('logits must be fp32 with unit column stride')
+    if t_dev.dtype != torch.int32 or not t_dev.is_cuda:
+        raise ValueError('t_dev must be an int32 device tensor')
+    n, k = logits.shape
+    L = _lib.load()
+    _lib.check(L.d1_sample_dev(logits.data_ptr(), n, k, logits.stride(0), seed, t_dev.data_ptr(), t_add & 0xFFFFFFFF,
+                               actions.data_ptr(), logp.data_ptr(),
+                               torch.cuda.current_stream(logits.device).cuda_stream), 'd1_sample_dev')
     return actions, logp
 
 

@@ -141,6 +141,13 @@ int d1_los_table(const uint8_t *floor, int n_maps, const D1Tables *rays, uint32_
  * else k-1. Writes int64 actions and fp32 log-probabilities (either may be null). */
 int d1_sample(const float *logits, int n, int k, int ld, uint64_t seed, uint32_t t,
               int64_t *actions, float *logp, void *stream);
+/* d1_sample with the counter step read from device memory: t = *t_dev + t_add (same
+ * result as d1_sample with that t). A rollout captured in a HIP graph keeps its step
+ * counter on the device and advances it on the device, so every replay samples new
+ * steps (the reference's loop draws from torch's generator at every call,
+ * gpu-d1/scripts/run_ring_ablations.py:350). */
+int d1_sample_dev(const float *logits, int n, int k, int ld, uint64_t seed, const uint32_t *t_dev, uint32_t t_add,
+                  int64_t *actions, float *logp, void *stream);
 
 /* Autoregressive two-stage sample (the type-then-direction head of
  * gpu-d1/branches/autoregressive-actions-v1/scripts/tactical_models.py:8-30, generalised

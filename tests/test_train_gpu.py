@@ -1,0 +1,99 @@
+"""The training loop (dcss-auto_amd/train.py): graph-captured rollouts equal eager ones,
+a resumed run equals the uninterrupted run bit for bit (the reference's
+gpu-d1/scripts/test_resume.py checks the same of its trainer), evaluation ends every
+episode, and the device-counter sampler equals the host-counter one."""
+import importlib
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def make_trainer(pkg, graph, n=2048, T=8, seed=11):
+    train = importlib.import_module('dcss-auto_amd.train')
+    P = importlib.import_module('dcss-auto_amd.policy')
+    env = pkg.Env(n, pkg.baseline_config(8), seed=seed, hash=False)
+    model = P.Policy(seed=2).cuda()
+    return train.Trainer(env, model, horizon=T, minibatch=8192, epochs=2, graph=graph)
+
+
+def test_sample_dev_matches_sample():
+    P = importlib.import_module('dcss-auto_amd.policy')
+    print('[train] sample_dev', flush=True)
+    g = torch.Generator().manual_seed(3)
+    logits = (torch.randn(5000, 16, generator=g) * 2).cuda()
+    a1, l1 = P.sample(logits, 99, 12)
+    t_dev = torch.tensor([5], dtype=torch.int32, device='cuda')
+    a2 = torch.empty_like(a1)
+    l2 = torch.empty_like(l1)
+    P.sample_dev(logits, 99, t_dev, 7, a2, l2)
+    assert torch.equal(a1, a2) and torch.equal(l1, l2)
+    # a counter near 2^32 wraps as uint32 on both paths
+    a3, l3 = P.sample(logits, 99, 2)
+    t_dev.fill_(-1)
+    P.sample_dev(logits, 99, t_dev, 3, a2, l2)
+    assert torch.equal(a3, a2) and torch.equal(l3, l2)
+
+
+def _buffers(tr):
+    b = tr.buf
+    return [b.obs, b.actions, b.logp, b.values, b.rewards, b.dones, b.bootstrap, tr.next_obs, tr.env.state, tr.t_dev]
+
+
+def test_graph_rollout_matches_eager(pkg):
+    """Three rollout+update rounds: the graph-replayed rollout equals eager launches bit for
+    bit every round, with eager torch work (GAE reductions, the PPO update) in between."""
+    print('[train] graph vs eager', flush=True)
+    eager = make_trainer(pkg, graph=False)
+    graph = make_trainer(pkg, graph=True)
+    for r in range(3):
+        eager.rollout()
+        graph.rollout()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(_buffers(eager), _buffers(graph))):
+            assert torch.equal(a, b), f'round {r}: buffer {i} differs'
+        eager.update()
+        graph.update()
+    assert torch.equal(eager.ppo.flat.p, graph.ppo.flat.p)
+    assert eager.buf.dones.sum() > 0 or eager.buf.rewards.abs().sum() > 0
+
+
+def test_resume_is_bit_exact(pkg, tmp_path):
+    """4 updates uninterrupted == 2 updates, save, a fresh trainer (other env seed) that
+    loads the checkpoint, 2 more updates: weights, Adam state, live worlds, observations,
+    counters and the shuffle generator all equal."""
+    print('[train] resume', flush=True)
+    full = make_trainer(pkg, graph=True)
+    full.train(4)
+    half = make_trainer(pkg, graph=True)
+    half.train(2)
+    half.save(tmp_path / 'ckpt.pt')
+    resumed = make_trainer(pkg, graph=True, seed=12345)
+    resumed.load(tmp_path / 'ckpt.pt')
+    resumed.train(2)
+    torch.cuda.synchronize()
+    a, b = full.state_dict(), resumed.state_dict()
+    for key in a:
+        if key == 'gen':
+            assert torch.equal(a[key], b[key]), key
+        else:
+            assert torch.equal(a[key], b[key]), key
+    assert int(a['updates']) == 4 and int(a['decisions']) == 4 * 8 * 2048
+    # the weights moved, and sync_model writes them into the module
+    model = resumed.sync_model()
+    assert torch.equal(model.l1.weight.detach().reshape(-1), resumed.ppo.flat.view(resumed.ppo.flat.p, 'l1.weight').reshape(-1))
+
+
+def test_evaluation_ends_every_episode(pkg):
+    print('[train] evaluation', flush=True)
+    tr = make_trainer(pkg, graph=False, n=1024)
+    ev = pkg.Env(256, pkg.baseline_config(8), seed=5, hash=False)
+    for mode in ('greedy', 'sampled'):
+        m = tr.evaluate(ev, mode)
+        print(f'[train] {mode}: {m}', flush=True)
+        assert 0.0 <= m['clear_rate'] <= 1.0 and 0.0 <= m['death_rate'] <= 1.0 and 0.0 <= m['timeout_rate'] <= 1.0
+        assert abs(m['clear_rate'] + m['death_rate'] + m['timeout_rate'] - 1.0) < 1e-6   # every episode ended one way
+        assert m['turns'] >= 1
+    # the same evaluation twice gives the same numbers (reset + counter RNG)
+    assert tr.evaluate(ev, 'sampled') == tr.evaluate(ev, 'sampled')
