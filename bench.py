@@ -108,6 +108,30 @@ def ppo_bench(args, env, rollout_model, policy_mod, dev):
                      'frac': flops / dt / 1e12 / BF16_PEAK_TFLOPS}}
 
 
+def train_bench(args, dev, updates=2):
+    """End-to-end PPO training at C3/C4's shapes: every update is a T=128 rollout over
+    65,536 worlds (one HIP-graph replay of T x (forward, sample, env step)) and the C4
+    update (GAE + 4 epochs of 8,192-sample minibatches); one warm-up update (graph
+    captures), then `updates` timed."""
+    import torch
+    pkg = importlib.import_module('dcss-auto_amd')
+    P = importlib.import_module('dcss-auto_amd.policy')
+    train = importlib.import_module('dcss-auto_amd.train')
+    env = pkg.Env(args.envs, pkg.baseline_config(args.monsters), seed=1, hash=False)
+    tr = train.Trainer(env, P.Policy(seed=0).to(dev), horizon=args.horizon)
+    tr.train(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tr.train(updates)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    decisions = updates * args.horizon * args.envs
+    return {'metric': 'PPO training decisions/s (T=128 rollout + 4-epoch update per iteration)', 'value': decisions / dt,
+            'unit': 'decisions/s', 's_per_update': dt / updates, 'updates': updates, 'path': 'graph rollout + graph PPO',
+            'config': {'workload': 'C3 rollout + C4 update', 'envs': args.envs, 'T': args.horizon, 'epochs': tr.ppo.epochs,
+                       'minibatch': tr.ppo.minibatch}}
+
+
 REFERENCE_WAITS_PER_S = 10.165e6   # gpu-d1/RESULTS.md:16, warp per world, RTX 5000 Max-Q
 
 
@@ -248,12 +272,13 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'wait', 'stress', 'learn'], default='rollout',
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'train', 'wait', 'stress', 'learn'], default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
-                         'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer')
+                         'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer; '
+                         'train: rollout + update iterations of the training loop')
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
     ap.add_argument('--eager-ppo', action='store_true', help='run the PPO update without HIP-graph capture')
-    ap.add_argument('--no-ppo', action='store_true', help='rollout mode: skip the C4 PPO measurement that follows')
+    ap.add_argument('--no-ppo', action='store_true', help='rollout mode: skip the C4 PPO and training measurements that follow')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
@@ -268,6 +293,9 @@ def main():
         return
     if args.mode == 'learn':
         print(json.dumps(learn_bench(args)), flush=True)
+        return
+    if args.mode == 'train':
+        print(json.dumps(train_bench(args, torch.device('cuda:0'))), flush=True)
         return
     pkg = importlib.import_module('dcss-auto_amd')
     policy_mod = importlib.import_module('dcss-auto_amd.policy')
@@ -348,6 +376,8 @@ def main():
         ppo = ppo_bench(args, env, model, policy_mod, dev)
         result['ppo'] = {k: ppo[k] for k in ('metric', 'value', 'unit', 'update_s', 'sample_epochs_per_s', 'dtype',
                                              'path', 'config', 'mfma')}
+        del ppo
+        result['train'] = train_bench(args, dev)
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline()
     print(json.dumps(result), flush=True)
