@@ -12,7 +12,8 @@ CSRC = HERE / 'csrc'
 FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared', '-ffp-contract=off',
          '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops']
 TARGETS = {
-    'libd1hip.so': ([CSRC / 'd1_env.hip', CSRC / 'd1_policy.hip', CSRC / 'd1_forward.hip', CSRC / 'd1_ppo.hip'], []),
+    'libd1hip.so': ([CSRC / 'd1_env.hip', CSRC / 'd1_policy.hip', CSRC / 'd1_forward.hip', CSRC / 'd1_ppo.hip',
+                     CSRC / 'd1_maps.hip'], []),
     'libd1learn_clump0.so': ([CSRC / 'd1_learn.hip'], ['-DD1_CLUMP_MODE=0']),
     'libd1learn_clump1.so': ([CSRC / 'd1_learn.hip'], ['-DD1_CLUMP_MODE=1']),
 }

@@ -47,6 +47,16 @@ class LearnMaps:
         _lib.check(_lib.load().d1_los_table(self.floor.data_ptr(), self.n_maps, C.byref(rays), self.los.data_ptr(),
                                             stream), 'd1_los_table')
 
+    @classmethod
+    def from_maps(cls, maps, device='cuda'):
+        """Tables from read_maps() output (corpus map files): their floors, with the LOS
+        table the map files carry, as the reference's EnvV2 uploads them
+        (gpu-d1/scripts/learn_env_v2.py:91-104)."""
+        self = cls(np.stack([m['floor'] for m in maps]), device)
+        los = np.ascontiguousarray(np.stack([m['los'] for m in maps]), np.uint32)
+        self.los.copy_(torch.from_numpy(los.view(np.int32)).to(self.device))
+        return self
+
     def tables(self, map_filter=-1):
         """The library's Tables struct; index/distance are not read by this library."""
         if not -2 <= map_filter < self.n_maps:

@@ -133,6 +133,13 @@ int d1_wait_run(void *worlds, int n, int count, const D1Config *cfg, const D1Wai
  * is the `los` table of the learning-task library (include/d1learn.h). */
 int d1_los_table(const uint8_t *floor, int n_maps, const D1Tables *rays, uint32_t *los, void *stream);
 
+/* Map compiler's distance rows (gpu-d1/scripts/compile_corpus.py:30-52,
+ * gpu-d1/scripts/compile_fixture.py:50-66): for each of the n source cells, BFS over the
+ * 8-connected floor cells of floor[5600] (nonzero = floor); dist[i*5600 + p] = the BFS
+ * distance of cell p from sources[i], 65535 where unreached (every cell of the row is
+ * written; a source outside 0..5599 leaves its row unreached). */
+int d1_distance_rows(const uint8_t *floor, const int16_t *sources, int n, uint16_t *dist, void *stream);
+
 /* Categorical sampling with the counter RNG; replaces torch.distributions.Categorical
  * sample/log_prob in the rollout (gpu-d1/scripts/run_ring_ablations.py:350-351).
  * logits: float [n, k] (row stride `ld` floats), 1 <= k <= 64. For env i the uniform
