@@ -160,6 +160,27 @@ __global__ __launch_bounds__(256) void k_u8_bf16(const uint4 *__restrict__ in, u
     out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
+// D4 camera transform of uint8 [n][15][15][8] observations: group g (0..7) mirrors x when
+// g >= 4, then turns the window g % 4 quarter turns ((x, y) -> (-y, x) each, x east, y
+// south, relative to the centre cell); out cell T_g(c) takes in cell c's 8 bytes. One
+// lane per (env, cell) moves 8 bytes.
+__global__ __launch_bounds__(256) void k_obs_d4(const uint8_t *__restrict__ obs, const int32_t *__restrict__ groups,
+                                                int n, uint8_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * 225) return;
+    const int env = (int)(i / 225), c = (int)(i - (int64_t)env * 225);
+    const int g = groups[env] & 7;
+    int x = c % 15 - 7, y = c / 15 - 7;
+    if (g >= 4) x = -x;
+    for (int r = 0; r < (g & 3); r++) {
+        const int t = x;
+        x = -y;
+        y = t;
+    }
+    const uint64_t v = *(const uint64_t *)(obs + i * 8);
+    *(uint64_t *)(out + ((int64_t)env * 225 + (y + 7) * 15 + x + 7) * 8) = v;
+}
+
 }  // namespace d1p
 
 extern "C" {
@@ -177,6 +198,15 @@ int d1_sample_dev(const float *logits, int n, int k, int ld, uint64_t seed, cons
     if (n == 0) return 0;
     hipLaunchKernelGGL(d1p::k_sample_dev, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, logits, n, k, ld,
                        (uint32_t)seed, (uint32_t)(seed >> 32), t_dev, t_add, actions, logp);
+    return (int)hipGetLastError();
+}
+int d1_obs_d4(const uint8_t *obs, const int32_t *groups, int n, uint8_t *out, void *stream) {
+    if (n < 0 || (n && (!obs || !groups || !out)) || (uintptr_t)obs % 8 || (uintptr_t)out % 8) return D1_E_ARG;
+    if (obs == out && n) return D1_E_ARG;   // a permutation needs a separate destination
+    if (n == 0) return 0;
+    const int64_t lanes = (int64_t)n * 225;
+    hipLaunchKernelGGL(d1p::k_obs_d4, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, (hipStream_t)stream, obs,
+                       groups, n, out);
     return (int)hipGetLastError();
 }
 int d1_sample_ar(const float *verb_logits, int nv, int ldv, const float *target_logits, int nt, int ldt, int n,

@@ -182,6 +182,13 @@ int d1_policy_pack(const void *w1, const void *w2, const void *w3, void *wpk, vo
 int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
                   float *logits, float *value, void *stream);
 
+/* D4 camera augmentation of the uint8 observation (the reference's EpisodeSymmetry,
+ * gpu-d1/branches/autoregressive-actions-v1/scripts/symmetry.py:10-70, restated for the
+ * 15x15x8 window): for env i with group g = groups[i] (0..7; x mirrored when g >= 4, then
+ * g%4 quarter turns (x, y) -> (-y, x) about the centre cell, x east, y south), out cell
+ * T_g(c) = obs cell c (all 8 channels). obs and out are distinct, 8-byte aligned. */
+int d1_obs_d4(const uint8_t *obs, const int32_t *groups, int n, uint8_t *out, void *stream);
+
 /* Widen `count` uint8 observation bytes to bf16 (exact), for the policy trunk.
  * count must be a multiple of 16 and both pointers 16-byte aligned. */
 int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stream);
