@@ -132,6 +132,39 @@ def train_bench(args, dev, updates=2):
                        'minibatch': tr.ppo.minibatch}}
 
 
+REFERENCE_PANEL_S = 2.312   # gpu-d1/PERFORMANCE.md:29: fixed panel with frozen worlds, median of three
+
+
+def panel_bench(args):
+    """The reference's fixed-panel evaluation harness (gpu-d1/scripts/benchmark_evaluation.py):
+    1,024 learning-task worlds on 32 maps (map_filter -2: 32 episodes per map), 1,024
+    decisions with finished worlds frozen, median of three after a warm-up. The reference's
+    32 validation maps and trained checkpoint are not in its repository: the maps here are
+    32 generated levels and the policies are the task's heuristic controller and a
+    random-init policy of the reference's shape, so outcome rates differ from its run."""
+    import statistics
+    import torch
+    pkg = importlib.import_module('dcss-auto_amd')
+    learn = importlib.import_module('dcss-auto_amd.learn')
+    floors = pkg.Env(32, pkg.baseline_config(8), seed=21, hash=False).floors()
+    env = learn.LearnEnv(1024, maps=learn.LearnMaps(floors), map_filter=-2, limit=2048, clump=1)
+    policy = learn.MaskedPolicy().cuda()
+    out = {}
+    for name, pol in (('heuristic', 'heuristic'), ('policy', policy)):
+        learn.evaluate_panel(env, pol, decisions=64)   # warm-up
+        runs = [learn.evaluate_panel(env, pol, decisions=1024, active=True) for _ in range(3)]
+        sec = statistics.median(r['seconds'] for r in runs)
+        r = runs[0]
+        out[name] = {'seconds': sec, 'clear_rate': r['clear_rate'], 'death_rate': r['death_rate'], 'kills': r['kills'],
+                     'unfinished': r['unfinished']}
+    return {'metric': 'fixed-panel evaluation seconds (1,024 worlds = 32 maps x 32 episodes, 1,024 decisions, frozen worlds)',
+            'value': out['policy']['seconds'], 'unit': 's', 'higher_is_better': False, 'n_gpus': 1,
+            'reference': {'value': REFERENCE_PANEL_S, 'source': 'gpu-d1/PERFORMANCE.md:29',
+                          'note': 'trained policy on the 32 validation maps, its own GPU'},
+            'runs': out, 'config': {'workload': 'panel', 'maps': 'generated', 'worlds': 1024, 'decisions': 1024,
+                                    'limit': 2048}}
+
+
 REFERENCE_WAITS_PER_S = 10.165e6   # gpu-d1/RESULTS.md:16, warp per world, RTX 5000 Max-Q
 
 
@@ -272,7 +305,8 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'train', 'wait', 'stress', 'learn'], default='rollout',
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'train', 'panel', 'wait', 'stress', 'learn'],
+                    default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
                          'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer; '
                          'train: rollout + update iterations of the training loop')
@@ -293,6 +327,9 @@ def main():
         return
     if args.mode == 'learn':
         print(json.dumps(learn_bench(args)), flush=True)
+        return
+    if args.mode == 'panel':
+        print(json.dumps(panel_bench(args)), flush=True)
         return
     if args.mode == 'train':
         print(json.dumps(train_bench(args, torch.device('cuda:0'))), flush=True)

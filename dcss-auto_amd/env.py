@@ -43,6 +43,15 @@ class Env:
         self.hash = torch.zeros(batch, dtype=torch.int32, device=self.device)
         self.reset(seed)
 
+    def floors(self):
+        """Each world's level floor as uint8 [batch, 5600] (1 = floor), unpacked from the
+        state rows (the 840-byte floor bitmap after the header, view, monsters and
+        viewed bitmap)."""
+        off = 96 + 8 * self.max_monsters + 840
+        words = self.state[:, off:off + 840].cpu().numpy().view('<u4').reshape(self.batch, 70, 3)
+        bits = np.unpackbits(words.view(np.uint8).reshape(self.batch, 70, 12), axis=2, bitorder='little')
+        return np.ascontiguousarray(bits[:, :, :80].reshape(self.batch, 5600))
+
     @property
     def stream(self):
         return torch.cuda.current_stream(self.device).cuda_stream

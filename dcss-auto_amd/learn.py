@@ -10,6 +10,7 @@ and the LOS table by the HIP LOS compiler (`d1_los_table`). There is no host pat
 the library refuses `gpu=0` and this module needs a GPU device.
 """
 import ctypes as C
+import time
 
 import numpy as np
 import torch
@@ -152,3 +153,64 @@ def bitmap_cells(words):
     w = np.asarray(words, np.uint32).reshape(70, 3)
     bits = ((w[:, :, None] >> np.arange(32, dtype=np.uint32)) & 1).reshape(70, 96)[:, :80]
     return bits.reshape(-1).astype(bool)
+
+
+class MaskedPolicy(torch.nn.Module):
+    """The policy shape of the reference's evaluation and pipeline benchmarks
+    (gpu-d1/scripts/benchmark_pipeline.py:9-16): obs -> 128 tanh -> 128 tanh -> action
+    logits with the invalid actions masked to -1e9, and a value."""
+
+    def __init__(self, obs=1015, actions=19, width=128, seed=0):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.body = torch.nn.Sequential(torch.nn.Linear(obs, width), torch.nn.Tanh(), torch.nn.Linear(width, width),
+                                        torch.nn.Tanh())
+        self.actor, self.critic = torch.nn.Linear(width, actions), torch.nn.Linear(width, 1)
+        with torch.no_grad():
+            for layer in (self.body[0], self.body[2], self.actor, self.critic):
+                layer.weight.copy_(torch.randn(layer.weight.shape, generator=g) / layer.in_features ** 0.5)
+                layer.bias.zero_()
+
+    def forward(self, obs, mask):
+        h = self.body(obs)
+        return self.actor(h).masked_fill(mask == 0, -1e9), self.critic(h).squeeze(-1)
+
+
+@torch.no_grad()
+def evaluate_panel(env, policy, decisions=1024, seed=900000, active=True, greedy=False):
+    """The reference's fixed-panel evaluation (gpu-d1/scripts/benchmark_evaluation.py,
+    gpu-d1/scripts/run_ring_ablations.py:231-267): reset the panel to `seed`, sample (or
+    take the most likely) masked action of `policy` — or the task's heuristic controller
+    when policy == 'heuristic' — for `decisions` steps with torch's RNG seeded to `seed`, freezing finished worlds through `active` when asked, and keep each world's
+    first terminal out row. Returns the wall time, the outcome rates and the per-map
+    rates (world i plays map i % n_maps under map_filter -2)."""
+    env.reset(seed)
+    n = env.batch
+    live = torch.ones(n, dtype=torch.bool, device=env.device)
+    terminal = torch.zeros_like(env.out)
+    returns = torch.zeros(n, device=env.device)
+    with torch.random.fork_rng(devices=[env.device]):
+        torch.manual_seed(seed)
+        torch.cuda.synchronize(env.device)
+        start = time.perf_counter()
+        for _ in range(decisions):
+            if policy == 'heuristic':   # the task's own controller (learn_heuristic)
+                action = env.heuristic()
+            else:
+                logits, _ = policy(env.obs, env.mask)
+                action = logits.argmax(-1) if greedy else torch.distributions.Categorical(logits=logits).sample()
+            _, out = env.step(action, active=live if active else None)
+            returns += live * out[:, 0]
+            ended = live & (out[:, 1] > 0)
+            terminal[ended] = out[ended]
+            live &= ~ended
+        torch.cuda.synchronize(env.device)
+        seconds = time.perf_counter() - start
+    t, r, unfinished = terminal.cpu(), returns.cpu(), int(live.sum())
+
+    def rates(tt, rr):
+        return dict(clear_rate=tt[:, 2].mean().item(), death_rate=tt[:, 6].mean().item(),
+                    kills=tt[:, 3].mean().item(), shaped_return=rr.mean().item())
+    k = env.maps.n_maps
+    return dict(seconds=seconds, unfinished=unfinished, **rates(t, r),
+                maps=[rates(t[i::k], r[i::k]) for i in range(k)])
