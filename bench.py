@@ -360,17 +360,18 @@ def main():
         print(json.dumps(ppo_bench(args, env, model, policy_mod, dev)), flush=True)
         return
 
-    def one_step(t, ev=None):
+    wpk, b1, b2, b3 = model.packed()
+    value = torch.empty(n, dtype=torch.float32, device=dev)
+
+    def one_step(t, ev=None):   # env step, then forward + counter-RNG sample in one kernel
         if ev is not None:
             ev[0].record()
         env.step(actions)
         if ev is not None:
             ev[1].record()
-        with torch.no_grad():
-            logits, value = model(env.obs)
+        policy_mod.policy_fwd_sample(env.obs.view(n, -1), wpk, b1, b2, b3, seed, t, actions, logp, value)
         if ev is not None:
             ev[2].record()
-        policy_mod.sample(logits, seed, t, actions, logp)
 
     for t in range(args.warmup):
         one_step(t)

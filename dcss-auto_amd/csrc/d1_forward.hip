@@ -27,6 +27,7 @@
 
 #include "../../include/d1hip.h"
 #include "d1_frag.h"
+#include "d1_sample.h"
 
 namespace d1t {
 
@@ -49,10 +50,16 @@ __host__ __device__ constexpr int kperm(int s, int h, int j) {
     return 32 * (s >> 1) + 16 * (s & 1) + 8 * (j >> 2) + 4 * h + (j & 3);
 }
 
+// SAMPLE: the epilogue also draws each sample's action with the counter-RNG sampler
+// (d1_sample.h, the arithmetic of d1_sample) at step t = (t_dev ? *t_dev : 0) + t_add;
+// logits may then be null.
+template <bool SAMPLE>
 __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs, int M, const uint16_t *__restrict__ wpk,
                                                 const uint16_t *__restrict__ b1, const uint16_t *__restrict__ b2,
                                                 const uint16_t *__restrict__ b3, float *__restrict__ logits,
-                                                float *__restrict__ value) {
+                                                float *__restrict__ value, uint32_t key0, uint32_t key1,
+                                                const uint32_t *__restrict__ t_dev, uint32_t t_add,
+                                                int64_t *__restrict__ actions, float *__restrict__ logp) {
     __shared__ __align__(16) uint8_t lds[LDS_BYTES];
     const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
     u32x4 *stage = (u32x4 *)lds;                           // W1 double buffer, later W2 + head
@@ -257,21 +264,65 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
         }
     }
     const uint16_t *b3l = bl + 512;
+    // the head output is bf16 (rounded once after the bias), widened to fp32; for sample block
+    // a this lane holds logits 4lh..4lh+3 (o[a][0..3]) and 8+4lh..8+4lh+3 (o[a][4..7]), lane
+    // half 0 the value
+    float o[2][8], v[2];
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+#pragma unroll
+        for (int g = 0; g < 2; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[a][4 * g + i] = bf(rb(z[a][4 * g + i] + bf(b3l[8 * g + 4 * lh + i])));
+        v[a] = bf(rb(z[a][8] + bf(b3l[16])));
+    }
+    if (SAMPLE) {
+        // lane half h samples block a = h: it keeps its own half of that block's row and
+        // receives the other half from its partner lane (l ^ 32), which sends the half of
+        // the partner's own block that this lane lacks
+        const uint32_t tstep = (t_dev ? *t_dev : 0u) + t_add;
+        // value blends by mask (a ternary between array elements is turned into a run-time
+        // index into a stack copy of the array)
+        const uint32_t hm = 0u - (uint32_t)lh;
+        auto pick = [&](float if0, float if1) {
+            return __uint_as_float((__float_as_uint(if1) & hm) | (__float_as_uint(if0) & ~hm));
+        };
+        float p[8], l16[16];
+#pragma unroll
+        for (int j = 0; j < 8; j++) p[j] = __shfl_xor(pick(o[1][j], o[0][j]), 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            l16[i] = pick(o[0][i], p[i]);
+            l16[4 + i] = pick(p[i], o[1][i]);
+            l16[8 + i] = pick(o[0][4 + i], p[4 + i]);
+            l16[12 + i] = pick(p[4 + i], o[1][4 + i]);
+        }
+        const int m = m0 + 32 * lh + lr;
+        if (m < M) {
+            auto lg = [&](int j) {   // a select chain: no register array indexed at run time
+                float r = l16[0];
+#pragma unroll
+                for (int q = 1; q < 16; q++) r = j == q ? l16[q] : r;
+                return r;
+            };
+            int act;
+            float lp;
+            d1s::sample_core(lg, NA, key0, key1, tstep, (uint32_t)m, act, lp);
+            actions[m] = act;
+            logp[m] = lp;
+        }
+    }
 #pragma unroll
     for (int a = 0; a < 2; a++) {
         const int m = m0 + 32 * a + lr;
         if (m < M) {
-            // the head output is bf16 (rounded once after the bias), widened to fp32
+            if (!SAMPLE || logits) {
 #pragma unroll
-            for (int g = 0; g < 2; g++) {
-                float4 o;
-                o.x = bf(rb(z[a][4 * g + 0] + bf(b3l[8 * g + 4 * lh + 0])));
-                o.y = bf(rb(z[a][4 * g + 1] + bf(b3l[8 * g + 4 * lh + 1])));
-                o.z = bf(rb(z[a][4 * g + 2] + bf(b3l[8 * g + 4 * lh + 2])));
-                o.w = bf(rb(z[a][4 * g + 3] + bf(b3l[8 * g + 4 * lh + 3])));
-                *(float4 *)(logits + (size_t)m * NA + 8 * g + 4 * lh) = o;
+                for (int g = 0; g < 2; g++)
+                    *(float4 *)(logits + (size_t)m * NA + 8 * g + 4 * lh) =
+                        make_float4(o[a][4 * g], o[a][4 * g + 1], o[a][4 * g + 2], o[a][4 * g + 3]);
             }
-            if (lh == 0) value[m] = bf(rb(z[a][8] + bf(b3l[16])));
+            if (lh == 0) value[m] = v[a];
         }
     }
 }
@@ -315,8 +366,20 @@ extern "C" int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const v
     if (M < 0 || (M > 0 && (!obs || !wpk || !b1 || !b2 || !b3 || !logits || !value))) return D1_E_ARG;
     if ((uintptr_t)obs % 8 || (uintptr_t)wpk % 16 || (uintptr_t)logits % 16) return D1_E_ARG;
     if (M == 0) return 0;
-    hipLaunchKernelGGL(d1t::k_policy, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs, M,
-                       (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, logits,
-                       value);
+    hipLaunchKernelGGL(d1t::k_policy<false>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs,
+                       M, (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, logits,
+                       value, 0u, 0u, nullptr, 0u, nullptr, nullptr);
+    return (int)hipGetLastError();
+}
+
+extern "C" int d1_policy_fwd_sample(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2,
+                                    const void *b3, uint64_t seed, const uint32_t *t_dev, uint32_t t_add, float *logits,
+                                    float *value, int64_t *actions, float *logp, void *stream) {
+    if (M < 0 || (M > 0 && (!obs || !wpk || !b1 || !b2 || !b3 || !value || !actions || !logp))) return D1_E_ARG;
+    if ((uintptr_t)obs % 8 || (uintptr_t)wpk % 16 || (uintptr_t)logits % 16) return D1_E_ARG;
+    if (M == 0) return 0;
+    hipLaunchKernelGGL(d1t::k_policy<true>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs,
+                       M, (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, logits,
+                       value, (uint32_t)seed, (uint32_t)(seed >> 32), t_dev, t_add, actions, logp);
     return (int)hipGetLastError();
 }

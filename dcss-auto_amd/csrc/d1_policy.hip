@@ -8,40 +8,22 @@
 #include <stdint.h>
 
 #include "../../include/d1hip.h"
+#include "d1_sample.h"
 
 namespace d1p {
 
-__device__ inline uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0, uint32_t k1) {
-#pragma unroll
-    for (int r = 0; r < 10; r++) {
-        uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
-        uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
-        uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
-        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
-    }
-    return c0;
-}
+using d1s::philox_w0;
 
-// the sample of row i at counter step t (shared by the two entry points: identical results)
+// the sample of row i at counter step t (shared with the fused forward: identical results)
 __device__ __forceinline__ void sample_row(const float *__restrict__ logits, int i, int k, int ld, uint32_t key0,
                                            uint32_t key1, uint32_t t, int64_t *__restrict__ actions,
                                            float *__restrict__ logp) {
     const float *l = logits + (size_t)i * ld;
-    float m = l[0];
-    for (int j = 1; j < k; j++) m = fmaxf(m, l[j]);
-    float s = 0.f;
-    for (int j = 0; j < k; j++) s += expf(l[j] - m);
-    uint32_t w = philox_w0(0u, t, (uint32_t)i, 3u, key0, key1);
-    float u = (float)(w >> 8) * (1.0f / 16777216.0f);
-    float c = 0.f;
-    int a = k - 1;
-    for (int j = 0; j < k; j++) {
-        c += expf(l[j] - m) / s;
-        if (u < c) { a = j; break; }
-    }
+    int a;
+    float lp;
+    d1s::sample_core([&](int j) { return l[j]; }, k, key0, key1, t, (uint32_t)i, a, lp);
     if (actions) actions[i] = a;
-    if (logp) logp[i] = l[a] - m - logf(s);
+    if (logp) logp[i] = lp;
 }
 
 __global__ __launch_bounds__(256) void k_sample(const float *__restrict__ logits, int n, int k, int ld, uint32_t key0,

@@ -1,0 +1,50 @@
+// d1hip: the categorical sampler's per-row arithmetic, shared by the standalone sampler
+// (d1_policy.hip) and the policy forward's fused epilogue (d1_forward.hip) so that both
+// give bit-identical actions and log-probabilities. Both files are built with
+// -ffp-contract=off.
+//
+// Row i at counter step t: u = (w >> 8) * 2^-24 with w = word 0 of
+// Philox4x32-10(ctr = {0, t, i, 3}, key = {key0, key1}) (Salmon et al., SC'11: multipliers
+// 0xD2511F53 / 0xCD9E8D57, Weyl increments 0x9E3779B9 / 0xBB67AE85); the action is the
+// first j with u < sum_{j' <= j} exp(l_j' - max) / sum exp(l - max) (fp32, left to right),
+// else k - 1; log p = l_a - max - log(sum).
+#ifndef D1_SAMPLE_H
+#define D1_SAMPLE_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace d1s {
+
+__device__ inline uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; r++) {
+        uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+        uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+        uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+    }
+    return c0;
+}
+
+// l(j) returns logit j of the row (global memory or registers)
+template <class L>
+__device__ __forceinline__ void sample_core(L l, int k, uint32_t key0, uint32_t key1, uint32_t t, uint32_t i, int &a,
+                                            float &lp) {
+    float m = l(0);
+    for (int j = 1; j < k; j++) m = fmaxf(m, l(j));
+    float s = 0.f;
+    for (int j = 0; j < k; j++) s += expf(l(j) - m);
+    const uint32_t w = philox_w0(0u, t, i, 3u, key0, key1);
+    const float u = (float)(w >> 8) * (1.0f / 16777216.0f);
+    float c = 0.f;
+    a = k - 1;
+    for (int j = 0; j < k; j++) {
+        c += expf(l(j) - m) / s;
+        if (u < c) { a = j; break; }
+    }
+    lp = l(a) - m - logf(s);
+}
+
+}  // namespace d1s
+#endif

@@ -96,6 +96,28 @@ def policy_fwd(obs_u8, wpk, b1, b2, b3, logits=None, value=None):
     return logits, value
 
 
+def policy_fwd_sample(obs_u8, wpk, b1, b2, b3, seed, t, actions, logp, value, t_dev=None, logits=None):
+    """policy_fwd and the counter-RNG sample of each row in one kernel (d1_policy_fwd_sample):
+    the same actions/log-probs as sample() / sample_dev() on policy_fwd's logits at step
+    t (+ t_dev[0] when given, int32 device tensor read as uint32)."""
+    obs_u8 = obs_u8.contiguous()
+    n = obs_u8.shape[0]
+    assert obs_u8.dtype == torch.uint8 and obs_u8.shape[1] == OBS
+    for b, size in ((b1, 256), (b2, 256), (b3, N_ACTIONS + 1)):
+        assert b.dtype == torch.bfloat16 and b.shape == (size,) and b.is_contiguous()
+    assert actions.dtype == torch.int64 and logp.dtype == torch.float32 and value.dtype == torch.float32
+    assert actions.numel() == n and logp.numel() == n and value.numel() == n
+    if t_dev is not None and t_dev.dtype != torch.int32:
+        raise ValueError('t_dev must be an int32 device tensor')
+    L = _lib.load()
+    _lib.check(L.d1_policy_fwd_sample(obs_u8.data_ptr(), n, wpk.data_ptr(), b1.data_ptr(), b2.data_ptr(), b3.data_ptr(),
+                                      seed, t_dev.data_ptr() if t_dev is not None else None, t & 0xFFFFFFFF,
+                                      logits.data_ptr() if logits is not None else None, value.data_ptr(),
+                                      actions.data_ptr(), logp.data_ptr(),
+                                      torch.cuda.current_stream(obs_u8.device).cuda_stream), 'd1_policy_fwd_sample')
+    return actions, logp, value
+
+
 def widen(obs_u8, dtype):
     """uint8 observations -> `dtype`; the bf16 case runs the HIP widening kernel."""
     if obs_u8.dtype != torch.uint8:

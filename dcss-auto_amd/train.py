@@ -1,13 +1,14 @@
 """PPO training loop on the batched environment: the drop-in for the reference's worker
 loop (gpu-d1/scripts/run_ring_ablations.py:185-388, gpu-d1/scripts/train_clear.py).
 
-One update = a T-step rollout (policy forward from the uint8 observation, counter-RNG
-sample, env step; each writes straight into the rollout buffer) followed by
-FastPPO.update (GAE, advantage normalisation, epochs of shuffled minibatches). With
-graph=True the whole rollout — T x (forward, sample, step, reward/done copies), the
+One update = a T-step rollout (policy forward from the uint8 observation with the
+counter-RNG sample in the same kernel, env step; each writes straight into the rollout
+buffer) followed by FastPPO.update (GAE, advantage normalisation, epochs of shuffled
+minibatches). With
+graph=True the whole rollout — T x (forward + sample, step, reward/done copies), the
 bootstrap value and the step-counter advance — is captured once in a HIP graph and
-replayed; the sampler reads its counter step from the device (d1_sample_dev), so every
-replay draws new actions.
+replayed; the sampler reads its counter step from the device, so every replay draws new
+actions.
 
 Checkpoints hold everything the next update reads: fp32 master weights, their bf16 copy,
 Adam moments and step, the live worlds (`env.state`) and their current observation, the
@@ -61,9 +62,9 @@ class Trainer:
         buf, env = self.buf, self.env
         b1, b2, b3 = self.bias
         buf.obs[0].copy_(self.next_obs)
-        for k in range(self.T):
-            P.policy_fwd(buf.obs[k], self.wpk, b1, b2, b3, logits=self.logits, value=buf.values[k])
-            P.sample_dev(self.logits, self.seed, self.t_dev, k, buf.actions[k], buf.logp[k])
+        for k in range(self.T):   # forward + sample in one kernel, the counter step read on the device
+            P.policy_fwd_sample(buf.obs[k], self.wpk, b1, b2, b3, self.seed, k, buf.actions[k], buf.logp[k],
+                                buf.values[k], t_dev=self.t_dev)
             dst = buf.obs[k + 1] if k + 1 < self.T else self.next_obs
             env.step(buf.actions[k], obs=dst)
             buf.rewards[k].copy_(env.out[:, 0])

@@ -181,6 +181,14 @@ int64_t d1_policy_packed_elems(void);
 int d1_policy_pack(const void *w1, const void *w2, const void *w3, void *wpk, void *stream);
 int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
                   float *logits, float *value, void *stream);
+/* d1_policy_fwd followed by the counter-RNG sample of every row in the same kernel: the
+ * actions and log-probabilities d1_sample / d1_sample_dev would draw from those logits at
+ * step t = (t_dev ? *t_dev : 0) + t_add (bit-identical), without the logits round trip
+ * through memory (logits may be null). Replaces policy forward + Categorical.sample /
+ * log_prob of the rollout loop (gpu-d1/scripts/run_ring_ablations.py:347-351). */
+int d1_policy_fwd_sample(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
+                         uint64_t seed, const uint32_t *t_dev, uint32_t t_add, float *logits, float *value,
+                         int64_t *actions, float *logp, void *stream);
 
 /* D4 camera augmentation of the uint8 observation (the reference's EpisodeSymmetry,
  * gpu-d1/branches/autoregressive-actions-v1/scripts/symmetry.py:10-70, restated for the

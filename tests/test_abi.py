@@ -19,7 +19,7 @@ def test_header_declares_the_abi():
                                          'd1_obs_to_bf16', 'd1_obs_d4', 'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step',
                                          'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
                                          'd1_sample_ar', 'd1_los_table', 'd1_distance_rows', 'd1_policy_packed_elems',
-                                         'd1_policy_pack', 'd1_policy_fwd'])
+                                         'd1_policy_pack', 'd1_policy_fwd', 'd1_policy_fwd_sample'])
     # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
     assert declared_symbols('d1learn.h', 'learn_') == sorted(
         ['learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size', 'learn_action_size',

@@ -350,3 +350,30 @@ def test_fast_ppo_update_tracks_autograd_ppo():
         cos = torch.nn.functional.cosine_similarity(d_ref, d_fast, dim=0).item()
         assert cos > 0.9, (name, cos)
     assert torch.isfinite(fast_terms).all()
+
+
+@pytest.mark.parametrize('M', [1, 255, 4133])
+def test_fused_sample_matches_forward_then_sampler(M):
+    """d1_policy_fwd_sample == d1_policy_fwd followed by d1_sample / d1_sample_dev, bit for
+    bit (actions, log-probabilities, value and logits), at a host step and a device step."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    print(f'[fused sample] M={M}', flush=True)
+    model = P.Policy(seed=8).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        for layer in (model.l1, model.l2, model.head):
+            layer.bias.copy_(torch.randn(layer.bias.shape) * 3)   # logits of varied scale
+    wpk, b1, b2, b3 = model.packed()
+    obs = torch.randint(0, 60, (M, 1800), dtype=torch.uint8, device='cuda')
+    logits, value = P.policy_fwd(obs, wpk, b1, b2, b3)
+    a_ref, lp_ref = P.sample(logits, 1234, 77)
+    a = torch.empty(M, dtype=torch.int64, device='cuda')
+    lp = torch.empty(M, device='cuda')
+    v = torch.empty(M, device='cuda')
+    lg = torch.empty(M, 16, device='cuda')
+    P.policy_fwd_sample(obs, wpk, b1, b2, b3, 1234, 77, a, lp, v, logits=lg)
+    assert torch.equal(a, a_ref) and torch.equal(lp, lp_ref) and torch.equal(v, value) and torch.equal(lg, logits)
+    t_dev = torch.tensor([70], dtype=torch.int32, device='cuda')
+    P.policy_fwd_sample(obs, wpk, b1, b2, b3, 1234, 7, a, lp, v, t_dev=t_dev)   # logits not written
+    assert torch.equal(a, a_ref) and torch.equal(lp, lp_ref)
+    if M >= 100:   # the rows do not all draw one action
+        assert len(torch.unique(a_ref)) > 4
