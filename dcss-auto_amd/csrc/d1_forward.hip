@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
     }
     __syncthreads();   // every wave is done with the W1 buffers before they are overwritten
 
-    // bias + ReLU + bf16 rounding of acc into B fragments: fragment s of sample block a takes
+    // bias + ReLU + bf16 rounding (hardware pack) of acc into B fragments: fragment s of sample block a takes
     // registers 8(s%2)..+7 of tile (a, s/2); register 4g + i is hidden unit 32b + 8g + 4lh + i
     bf16x8 hf[2][16];
     auto to_frags = [&](const uint16_t *bias) {
@@ -204,8 +204,10 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
 #pragma unroll
                 for (int a = 0; a < 2; a++) {
                     const int s = 2 * b + (g >> 1), j0 = 4 * (g & 1);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) hf[a][s][j0 + i] = __builtin_bit_cast(__bf16, rb_num(fmaxf(acc[a][b][4 * g + i] + bb[i], 0.f)));
+                    u32x4 w = __builtin_bit_cast(u32x4, hf[a][s]);
+                    w[j0 / 2] = cvt2(fmaxf(acc[a][b][4 * g] + bb[0], 0.f), fmaxf(acc[a][b][4 * g + 1] + bb[1], 0.f));
+                    w[j0 / 2 + 1] = cvt2(fmaxf(acc[a][b][4 * g + 2] + bb[2], 0.f), fmaxf(acc[a][b][4 * g + 3] + bb[3], 0.f));
+                    hf[a][s] = as_bf(w);
                 }
             }
     };
@@ -273,8 +275,13 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
 #pragma unroll
         for (int g = 0; g < 2; g++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) o[a][4 * g + i] = bf(rb(z[a][4 * g + i] + bf(b3l[8 * g + 4 * lh + i])));
-        v[a] = bf(rb(z[a][8] + bf(b3l[16])));
+            for (int i = 0; i < 4; i += 2) {
+                const uint32_t w = cvt2(z[a][4 * g + i] + bf(b3l[8 * g + 4 * lh + i]),
+                                        z[a][4 * g + i + 1] + bf(b3l[8 * g + 4 * lh + i + 1]));
+                o[a][4 * g + i] = __uint_as_float(w << 16);
+                o[a][4 * g + i + 1] = __uint_as_float(w & 0xFFFF0000u);
+            }
+        v[a] = __uint_as_float(cvt2(z[a][8] + bf(b3l[16]), 0.f) << 16);
     }
     if (SAMPLE) {
         // lane half h samples block a = h: it keeps its own half of that block's row and

@@ -47,6 +47,15 @@ __device__ __forceinline__ uint32_t widen2(uint32_t x, int s) {
     return lo | hi;
 }
 // four bytes -> four bf16 (exact): the high halves of the converted floats, paired by v_perm
+// two floats -> two bf16 in one dword (lo in bits 0-15) with the hardware pack
+// (v_cvt_pk_bf16_f32): round to nearest even, equal to rb() / rb_num() for every non-NaN
+// input (checked on the hardware over all denormals, ties, infinities and a 1/257
+// sample of all finite patterns); NaN in gives a quiet NaN.
+__device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
+    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+    const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
 __device__ __forceinline__ uint2 widen4(uint32_t x) {
     const uint32_t f0 = __float_as_uint((float)(x & 255u)), f1 = __float_as_uint((float)((x >> 8) & 255u));
     const uint32_t f2 = __float_as_uint((float)((x >> 16) & 255u)), f3 = __float_as_uint((float)(x >> 24));
