@@ -103,8 +103,13 @@ __device__ __forceinline__ float rows_out(const float (&v)[16], uint16_t *tile, 
     float colsum = 0.f;
     uint32_t pos = 0;
 #pragma unroll
+    for (int r = 0; r < 16; r += 2) {   // hardware pack, two values per instruction
+        const uint32_t w2 = cvt2(v[r], v[r + 1]);
+        hb[r] = (uint16_t)(w2 & 0xFFFFu);
+        hb[r + 1] = (uint16_t)(w2 >> 16);
+    }
+#pragma unroll
     for (int r = 0; r < 16; r++) {
-        hb[r] = rb(v[r]);
         colsum += bf(hb[r]);
         if (bf(hb[r]) > 0.f) pos |= 1u << r;
         if (tile) tile[drow(r, lh) * XS + c] = hb[r];
@@ -623,9 +628,11 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) s.x += x[j].x, s.y += x[j].y, s.z += x[j].z, s.w += x[j].w;
             }
-            const uint16_t h0 = rb(s.x), h1 = rb(s.y), h2 = rb(s.z), h3 = rb(s.w);
-            *(uint2 *)dst = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2 | ((uint32_t)h3 << 16));
-            sq += bf(h0) * bf(h0) + bf(h1) * bf(h1) + bf(h2) * bf(h2) + bf(h3) * bf(h3);
+            const uint32_t w01 = cvt2(s.x, s.y), w23 = cvt2(s.z, s.w);
+            *(uint2 *)dst = make_uint2(w01, w23);
+            const float h0 = __uint_as_float(w01 << 16), h1 = __uint_as_float(w01 & 0xFFFF0000u);
+            const float h2 = __uint_as_float(w23 << 16), h3 = __uint_as_float(w23 & 0xFFFF0000u);
+            sq += h0 * h0 + h1 * h1 + h2 * h2 + h3 * h3;
         }
     } else {   // biases: 8 columns per workgroup, 32 lanes per column over the row partials
         const int col = 8 * (blockIdx.x - NRED) + (t >> 5), part = t & 31, nrows = mb / R;
@@ -718,7 +725,12 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
             mm[e] = a.beta1 * mm[e] + (1.f - a.beta1) * gi;
             vq[e] = a.beta2 * vq[e] + (1.f - a.beta2) * gi * gi;
             pp[e] = pp[e] - step_size * mm[e] / (sqrtf(vq[e]) / bc2s + a.eps);
-            h[e] = rb(pp[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+            const uint32_t w2 = cvt2(pp[e], pp[e + 1]);
+            h[e] = (uint16_t)(w2 & 0xFFFFu);
+            h[e + 1] = (uint16_t)(w2 >> 16);
         }
         *(float4 *)(a.p + i0) = pv;
         *(float4 *)(a.m + i0) = mv;
