@@ -40,7 +40,7 @@ constexpr int XS = H + 8;             // LDS row stride (bf16) of the [32][256] 
 constexpr int DS = 40;                // LDS row stride (bf16) of the dz tile (32 columns used)
 constexpr int XR = K1 + 16;           // LDS row stride (bf16) of k_rows' x tile: 908 dwords, so the
                                       // 16-byte fragment reads of 16 consecutive rows hit distinct banks
-constexpr int BP = 544;               // bias partial row: db1[256] | db2[256] | db3[17] | pad
+constexpr int BP = 544;               // bias partial row: db1[256] | db2[256] | db3[17] | loss sum | pad
 constexpr int C1 = 29;                // layer-1 K chunks (28 of 64 + the 8 inputs 1792..1799)
 constexpr int XB = 57;                // 32-row blocks of the x copy (1824 rows, 1800..1823 zero)
 constexpr int KW = 1024;              // samples per dW1 / dW2 workgroup
@@ -345,6 +345,12 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         if (t < 3)
             for (int q = 0; q < 8; q++) s += lsum[q][t];
         a.loss_parts[(size_t)blockIdx.x * 4 + t] = s;
+        // the three loss sums also go to the bias-partial row's column 2H+NZ (k_reduce folds
+        // their finiteness into the gradient norm)
+        float z = s;
+        z += __shfl_xor(z, 1);
+        z += __shfl_xor(z, 2);
+        if (t == 0) w.bpart[(size_t)blockIdx.x * BP + 2 * H + NZ] = z;
     } else if (t >= 64 && t < 64 + NZ) {   // head-bias partial: the 8 waves' sums
         float s = 0.f;
 #pragma unroll
@@ -637,7 +643,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
     } else {   // biases: 8 columns per workgroup, 32 lanes per column over the row partials
         const int col = 8 * (blockIdx.x - NRED) + (t >> 5), part = t & 31, nrows = mb / R;
         float s = 0.f;
-        if (col < 2 * H + NZ)
+        if (col <= 2 * H + NZ)
             for (int r0 = part; r0 < nrows; r0 += 256) {   // eight loads in flight
                 float x[8];
 #pragma unroll
@@ -652,6 +658,11 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
             uint16_t *dst = col < H ? g + a.off_b1 + col : col < 2 * H ? g + a.off_b2 + (col - H) : g + a.off_b3 + (col - 2 * H);
             *dst = hb;
             sq = bf(hb) * bf(hb);
+        } else if (part == 0 && col == 2 * H + NZ) {
+            // the loss column: 0 * (minibatch loss sum) is +-0 when the loss is finite, which
+            // leaves the norm bit-identical, and NaN otherwise, so k_adam sees a non-finite
+            // loss as a non-finite norm
+            sq = 0.f * s;
         }
     }
     const float tot = block_sum(sq, red);
@@ -695,7 +706,11 @@ __device__ __forceinline__ void pack_param(const D1PPOStep &a, uint16_t *wpk, in
 
 // Global-norm clip + Adam (torch.optim.Adam, no weight decay) over the flat buffers. Every
 // workgroup re-sums the norm partials; t = step[1] (set by k_reduce); workgroup 0 stores it
-// back to step[0] and advances the minibatch cursor.
+// back to step[0] and advances the minibatch cursor. A non-finite norm (non-finite
+// gradients, or a non-finite loss folded in by k_reduce) leaves every parameter, moment and
+// the step count as they are and counts the step in step[2]; while step[2] is not zero
+// every later step is skipped the same way, so the weights stay those of the last step
+// before the first non-finite loss.
 __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     __shared__ float red[4];
     if (a.cursor[1] == 0) return;
@@ -711,6 +726,13 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     float acc = 0.f;
     for (int j = threadIdx.x; j < NRED + NBIASB; j += blockDim.x) acc += w.npart[j];
     const float norm = sqrtf(block_sum(acc, red));
+    if (!(norm <= 3.4028235e38f) || a.step[2] != 0.f) {   // NaN fails the comparison
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            a.step[2] += 1.f;
+            a.cursor[0] += 1;
+        }
+        return;
+    }
     const float coef = fminf(a.max_grad_norm / (norm + 1e-6f), 1.f);
     const float tt = a.step[1];
     const float bc1 = 1.f - powf(a.beta1, tt), bc2 = 1.f - powf(a.beta2, tt);

@@ -57,6 +57,8 @@ class PPO:
         with torch.autocast('cuda', dtype=torch.bfloat16, enabled=self.autocast):
             logits, value = self.model(obs)
         loss, pg, vl, ent = ppo_loss(logits, value, actions, old_logp, adv, ret, self.clip, self.vcoef, self.ecoef)
+        if not torch.isfinite(loss).item():   # as the reference's update loop (run_ring_ablations.py:369-370)
+            raise RuntimeError('Non-finite PPO loss')
         self.opt.zero_grad(set_to_none=True)
         loss.backward()
         torch.nn.utils.clip_grad_norm_(self.model.parameters(), self.max_grad_norm)
@@ -123,7 +125,12 @@ class FastPPO:
     forward/loss/backward, grouped split-K weight gradients, fixed-order reduction, clip +
     Adam). Same interface and semantics as PPO with bf16 autocast; `minibatch` must be a
     multiple of 1024. With graph=True, `graph_steps` consecutive minibatch steps are
-    captured in one HIP graph per buffer and replayed."""
+    captured in one HIP graph per buffer and replayed.
+
+    A minibatch whose loss or gradient norm is not finite changes nothing, and neither does
+    any later one until `clear_nonfinite()`; `update` then raises RuntimeError, as the
+    reference's loop does at the first non-finite loss (run_ring_ablations.py:369-370),
+    leaving the weights and Adam state of the last finite step."""
 
     def __init__(self, policy, lr=3e-4, eps=1e-5, clip=0.2, vcoef=0.5, ecoef=0.01, max_grad_norm=0.5,
                  epochs=4, minibatch=8192, gamma=0.99, lam=0.95, graph=True, graph_steps=16):
@@ -135,7 +142,7 @@ class FastPPO:
         self.lr, self.eps, self.clip, self.vcoef, self.ecoef = lr, eps, clip, vcoef, ecoef
         self.max_grad_norm, self.epochs, self.minibatch, self.gamma, self.lam = max_grad_norm, epochs, minibatch, gamma, lam
         self.graph, self.graph_steps, self.dev = graph, graph_steps, dev
-        self.step_t = torch.zeros(2, dtype=torch.float32, device=dev)
+        self.step_t = torch.zeros(3, dtype=torch.float32, device=dev)   # Adam step, scratch, skipped steps
         self.cursor = torch.zeros(2, dtype=torch.int32, device=dev)
         self.loss_parts = torch.zeros(minibatch // 32 * 4, dtype=torch.float32, device=dev)
         nbytes = _lib.load().d1_ppo_work_bytes(minibatch)
@@ -184,6 +191,13 @@ class FastPPO:
         from . import _lib
         args = self._struct(obs, actions, logp, adv, ret)
         _lib.check(_lib.load().d1_ppo_step(args, torch.cuda.current_stream(self.dev).cuda_stream), 'd1_ppo_step')
+
+    def nonfinite_steps(self):
+        """Minibatch steps skipped since the first non-finite loss or gradient norm."""
+        return int(self.step_t[2].item())
+
+    def clear_nonfinite(self):
+        self.step_t[2].zero_()
 
     def loss_terms(self):
         """(pg, value, entropy) means of the last minibatch (reads device partials)."""
@@ -241,4 +255,6 @@ class FastPPO:
             else:
                 for _ in range(steps):
                     self._step(obs, actions, logp, adv, ret)
+        if self.nonfinite_steps():
+            raise RuntimeError('Non-finite PPO loss')
         return self.loss_terms()

@@ -10,12 +10,19 @@ bootstrap value and the step-counter advance — is captured once in a HIP graph
 replayed; the sampler reads its counter step from the device, so every replay draws new
 actions.
 
+`run` is the worker loop around them: resume, periodic and stop-time checkpoints, a
+SIGTERM/SIGINT stop at an update boundary (exit status 130), an abort on a non-finite loss.
+
 Checkpoints hold everything the next update reads: fp32 master weights, their bf16 copy,
 Adam moments and step, the live worlds (`env.state`) and their current observation, the
 sampler's step counter and the minibatch-shuffle generator. A run resumed from one is
 bit-identical to the uninterrupted run (the reference's gpu-d1/scripts/test_resume.py
 checks the same for its trainer: weights, optimizer, live worlds, observations, RNGs).
 """
+import os
+import signal
+import threading
+
 import torch
 
 from . import _lib
@@ -102,6 +109,43 @@ class Trainer:
             terms = self.update()
         return terms
 
+    def run(self, decisions, checkpoint=None, checkpoint_every=None, on_update=None, handle_signals=True):
+        """The reference's worker loop (gpu-d1/scripts/run_ring_ablations.py:291-295,341-388):
+        resume from `checkpoint` when that file exists, then rollout + update until
+        `decisions` decisions have been trained, persisting to `checkpoint` every
+        `checkpoint_every` decisions and at the end. SIGTERM or SIGINT (when called from
+        the main thread with handle_signals) stops at the next update boundary, persists
+        and returns 130 — rerunning the same call resumes; a finished run returns 0. A
+        non-finite loss raises RuntimeError from `update`, with nothing persisted past the
+        last finite update. `on_update(trainer, terms)` runs after every update (logging,
+        milestone evaluation)."""
+        if checkpoint is not None and os.path.exists(checkpoint):
+            self.load(checkpoint)
+        stop = [False]
+        previous = {}
+        if handle_signals and threading.current_thread() is threading.main_thread():
+            def interrupt(*_):
+                stop[0] = True
+            for sig in (signal.SIGTERM, signal.SIGINT):
+                previous[sig] = signal.signal(sig, interrupt)
+        try:
+            every = checkpoint_every or 0
+            next_save = (self.decisions // every + 1) * every if every else None
+            while self.decisions < decisions and not stop[0]:
+                self.rollout()
+                terms = self.update()
+                if on_update is not None:
+                    on_update(self, terms)
+                if checkpoint is not None and next_save is not None and self.decisions >= next_save and not stop[0]:
+                    self.save(checkpoint)
+                    next_save = (self.decisions // every + 1) * every if every else None
+            if checkpoint is not None:
+                self.save(checkpoint)
+            return 130 if stop[0] else 0
+        finally:
+            for sig, handler in previous.items():
+                signal.signal(sig, handler)
+
     def sync_model(self):
         """Copy the fp32 master weights into the nn.Module."""
         self.ppo.flat.load_into(self.model)
@@ -128,7 +172,11 @@ class Trainer:
         self._repack()
 
     def save(self, path):
-        torch.save(self.state_dict(), path)
+        """Write the checkpoint atomically: a reader sees the previous file or the new one."""
+        path = os.fspath(path)
+        tmp = f'{path}.tmp{os.getpid()}'
+        torch.save(self.state_dict(), tmp)
+        os.replace(tmp, path)
 
     def load(self, path):
         self.load_state_dict(torch.load(path, map_location='cpu', weights_only=True))

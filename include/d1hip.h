@@ -233,7 +233,9 @@ typedef struct {
     float *m, *v;                   /* Adam moments */
     int64_t nparams;                /* a multiple of 4 */
     int64_t off_w1, off_b1, off_w2, off_b2, off_w3, off_b3;
-    float *step;                    /* [2] Adam step count (torch.optim.Adam semantics, no decay) */
+    float *step;                    /* [3]: [0] Adam step count (torch.optim.Adam semantics, no decay), [1] scratch,
+                                       [2] steps skipped since the first non-finite loss or gradient norm (sticky:
+                                       while non-zero every step is skipped; the caller clears it) */
     float *loss_parts;              /* [mb/32 * 4]: per 32 samples the sums of pg, 0.5*(v-R)^2, entropy */
     void *work;                     /* d1_ppo_work_bytes(mb) bytes of device memory, 256-byte aligned */
     int64_t work_bytes;

@@ -1,7 +1,8 @@
 """The training loop (dcss-auto_amd/train.py): graph-captured rollouts equal eager ones,
 a resumed run equals the uninterrupted run bit for bit (the reference's
-gpu-d1/scripts/test_resume.py checks the same of its trainer), evaluation ends every
-episode, and the device-counter sampler equals the host-counter one."""
+gpu-d1/scripts/test_resume.py checks the same of its trainer), also when the worker loop is
+stopped by SIGTERM, a non-finite loss stops the update with the last finite weights,
+evaluation ends every episode, and the device-counter sampler equals the host-counter one."""
 import importlib
 
 import pytest
@@ -97,3 +98,69 @@ def test_evaluation_ends_every_episode(pkg):
         assert m['turns'] >= 1
     # the same evaluation twice gives the same numbers (reset + counter RNG)
     assert tr.evaluate(ev, 'sampled') == tr.evaluate(ev, 'sampled')
+
+
+def test_non_finite_loss_leaves_the_last_finite_weights(pkg):
+    """A NaN reward makes every advantage NaN: FastPPO skips every minibatch step, keeps the
+    weights, moments, Adam step and packed copies of the last finite update, and update
+    raises as the reference's loop does; after clear_nonfinite training goes on."""
+    print('[train] non-finite loss', flush=True)
+    tr = make_trainer(pkg, graph=True)
+    tr.rollout()
+    tr.update()
+    F = tr.ppo.flat
+    keep = [F.p.clone(), F.pb.clone(), F.m.clone(), F.v.clone(), tr.ppo.step_t[:1].clone(), tr.wpk.clone()]
+    tr.rollout()
+    tr.buf.rewards[3, 17] = float('nan')
+    with pytest.raises(RuntimeError, match='Non-finite'):
+        tr.update()
+    steps = 2 * (8 * 2048 // 8192)
+    assert tr.ppo.nonfinite_steps() == steps
+    for i, (a, b) in enumerate(zip(keep, [F.p, F.pb, F.m, F.v, tr.ppo.step_t[:1], tr.wpk])):
+        assert torch.equal(a, b), i
+    tr.ppo.clear_nonfinite()
+    tr.rollout()
+    tr.update()
+    assert tr.ppo.nonfinite_steps() == 0 and not torch.equal(F.p, keep[0]) and bool(torch.isfinite(F.p).all())
+    assert float(tr.ppo.step_t[0]) == float(keep[4][0]) + steps
+
+
+def test_autograd_ppo_raises_on_a_non_finite_loss():
+    P = importlib.import_module('dcss-auto_amd.policy')
+    ppo_mod = importlib.import_module('dcss-auto_amd.ppo')
+    model = P.Policy(seed=3).cuda()
+    ppo = ppo_mod.PPO(model)
+    obs = torch.randint(0, 40, (64, 1800), dtype=torch.uint8, device='cuda')
+    act = torch.randint(0, 16, (64,), device='cuda')
+    logp = torch.full((64,), -2.77, device='cuda')
+    adv = torch.randn(64, device='cuda')
+    adv[5] = float('inf')
+    before = model.l1.weight.detach().clone()
+    with pytest.raises(RuntimeError, match='Non-finite'):
+        ppo.minibatch_step(obs, act, logp, adv, torch.zeros(64, device='cuda'))
+    assert torch.equal(model.l1.weight, before)
+
+
+def test_worker_loop_stop_and_resume_is_bit_exact(pkg, tmp_path):
+    """run() to 4 updates == run() stopped by SIGTERM after update 2 (status 130), then the
+    same call on a fresh trainer (other env seed), which resumes from the checkpoint."""
+    import os
+    import signal
+    print('[train] worker loop stop/resume', flush=True)
+    target = 4 * 8 * 2048
+    full = make_trainer(pkg, graph=True)
+    assert full.run(target, handle_signals=False) == 0
+    ck = tmp_path / 'latest.pt'
+    first = make_trainer(pkg, graph=True)
+
+    def hook(t, terms):
+        if t.updates == 2:
+            os.kill(os.getpid(), signal.SIGTERM)
+
+    assert first.run(target, checkpoint=ck, on_update=hook) == 130
+    resumed = make_trainer(pkg, graph=True, seed=12345)
+    assert resumed.run(target, checkpoint=ck) == 0
+    torch.cuda.synchronize()
+    a, b = full.state_dict(), resumed.state_dict()
+    for key in a:
+        assert torch.equal(a[key], b[key]), key
