@@ -420,65 +420,98 @@ struct KB {
     int sl0, sl1, sl2;   // stair layers, -1 = not reached
     int mlayer;          // this lane's monster layer
 };
-__device__ __forceinline__ Row kbfs_expand(const Smem *sm, int y) {
-    Row v = row_ld(sm->front, y);
-    if (y > 0) v = row_or(v, row_ld(sm->front, y - 1));
-    if (y < H - 1) v = row_or(v, row_ld(sm->front, y + 1));
-    v = row_or(v, row_or(row_shl1(v), row_shr1(v)));
-    Row pass = row_and(row_ld(sm->floor, y), row_ld(sm->viewed, y));
-    return row_andn(row_and(v, pass), row_ld(sm->reach, y));
-}
+// Lane l keeps rows l and (l < 6) 64 + l of the frontier, reach, known floor and anchors in
+// registers; vertical neighbours arrive by lane shuffles, so a layer needs no LDS round
+// trip and no barrier. The layer of every reached cell is scattered into sm->dist as it is
+// reached; reach, the last layer's frontier and the anchor rows are published at the end.
+__device__ __forceinline__ uint32_t row_word(Row r, int w) { return w == 0 ? r.a : w == 1 ? r.b : r.c; }
 __device__ __forceinline__ KB known_bfs(LCtx &c, bool want_anchor, int want_stairs, bool want_monster) {
     Ctx &x = c.x;
     Smem *sm = x.sm;
     LSmem *L = c.L;
+    const int lane = x.lane;
+    const bool has1 = lane < H - 64;
+    const Row zero{0, 0, 0};
     KB r{-1, -1, -1, -1, -1};
-    for (int w = x.lane; w < ROWS_WORDS; w += 64) { sm->reach[w] = 0; sm->front[w] = 0; }
-    __syncthreads();
-    if (x.lane == 0) {
-        int p = x.player;
-        sm->reach[(p / W) * RW + ((p % W) >> 5)] |= 1u << ((p % W) & 31);
-        sm->front[(p / W) * RW + ((p % W) >> 5)] |= 1u << ((p % W) & 31);
-        sm->dist[p] = 0;
+    __syncthreads();   // floor, viewed and anchor rows written by other lanes
+    const Row k0 = row_and(row_ld(sm->floor, lane), row_ld(sm->viewed, lane));
+    const Row k1 = has1 ? row_and(row_ld(sm->floor, 64 + lane), row_ld(sm->viewed, 64 + lane)) : zero;
+    Row a0 = zero, a1 = zero;
+    if (want_anchor) {
+        a0 = row_ld(L->anch, lane);
+        if (has1) a1 = row_ld(L->anch, 64 + lane);
     }
-    __syncthreads();
+    const int py = x.player / W, px = x.player % W;
+    const Row pbit = row_range(px, px);
+    Row f0 = lane == py ? pbit : zero, f1 = has1 && 64 + lane == py ? pbit : zero;
+    Row r0 = f0, r1 = f1;
+    if (lane == 0) sm->dist[x.player] = 0;
+    // wanted stairs: holder lane, register row and word of each (uniform)
     const int s0 = stair_at(x, 0), s1 = stair_at(x, 1), s2 = stair_at(x, 2);
-    const int y0 = x.lane, y1 = x.lane + 64;
+    // this lane's monster cell, when it is wanted: holder lane and word of its row
+    const bool mneed = want_monster && lane_alive(c) && in_view(x, x.mpos);
+    const int my = mneed ? x.mpos / W : 0, mx = mneed ? x.mpos % W : 0;
+    const int msrc = my & 63, mword = mx >> 5;
+    const uint32_t mbit = 1u << (mx & 31);
     for (int layer = 0; layer < N; layer++) {
         if (layer > 0) {
-            Row n0 = kbfs_expand(sm, y0), n1 = y1 < H ? kbfs_expand(sm, y1) : Row{0, 0, 0};
-            __syncthreads();
-            bfs_commit(sm, y0, n0, layer);
-            if (y1 < H) bfs_commit(sm, y1, n1, layer);
-            __syncthreads();
+            const Row f1_0 = row_lane(f1, 0), f0_63 = row_lane(f0, 63);
+            const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, f1_0, row_dn(f0));
+            const Row u1 = row_sel(lane == 0, f0_63, row_up(f1)), d1 = row_sel(lane >= H - 65, zero, row_dn(f1));
+            const Row n0 = row_andn(row_and(dilate(f0, u0, d0), k0), r0);
+            const Row n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), k1), r1) : zero;
+            r0 = row_or(r0, n0); r1 = row_or(r1, n1);
+            f0 = n0; f1 = n1;
+            scatter_layer(sm, lane * W, n0.a, layer);
+            scatter_layer(sm, lane * W + 32, n0.b, layer);
+            scatter_layer(sm, lane * W + 64, n0.c, layer);
+            if (has1) {
+                scatter_layer(sm, (64 + lane) * W, n1.a, layer);
+                scatter_layer(sm, (64 + lane) * W + 32, n1.b, layer);
+                scatter_layer(sm, (64 + lane) * W + 64, n1.c, layer);
+            }
             if (!ballot(row_any(n0) || row_any(n1))) break;
         }
         bool done = true;
         if (want_anchor && r.alayer < 0) {
-            Row h0 = row_and(row_ld(sm->front, y0), row_ld(L->anch, y0));
-            Row h1 = y1 < H ? row_and(row_ld(sm->front, y1), row_ld(L->anch, y1)) : Row{0, 0, 0};
+            const Row h0 = row_and(f0, a0), h1 = row_and(f1, a1);
             if (ballot(row_any(h0) || row_any(h1))) {
                 r.alayer = layer;
-                __syncthreads();
-                row_st(L->anch, y0, h0);
-                if (y1 < H) row_st(L->anch, y1, h1);
-                __syncthreads();
+                a0 = h0; a1 = h1;
             } else done = false;
         }
-        if (want_stairs & 1) { if (r.sl0 < 0 && bit(sm->reach, s0)) r.sl0 = layer; done = done && r.sl0 >= 0; }
-        if (want_stairs & 2) { if (r.sl1 < 0 && bit(sm->reach, s1)) r.sl1 = layer; done = done && r.sl1 >= 0; }
-        if (want_stairs & 4) { if (r.sl2 < 0 && bit(sm->reach, s2)) r.sl2 = layer; done = done && r.sl2 >= 0; }
+#define D1_STAIR_LAYER(bitmask, st, sl)                                                                       \
+        if (want_stairs & (bitmask)) {                                                                        \
+            if (sl < 0) {                                                                                     \
+                const int sy = (st) / W, sx = (st) % W;                                                      \
+                const uint32_t w = (uint32_t)lane_val((int)row_word(sy >= 64 ? r1 : r0, sx >> 5), sy & 63); \
+                if ((w >> (sx & 31)) & 1u) sl = layer;                                                        \
+            }                                                                                                 \
+            done = done && sl >= 0;                                                                           \
+        }
+        D1_STAIR_LAYER(1, s0, r.sl0)
+        D1_STAIR_LAYER(2, s1, r.sl1)
+        D1_STAIR_LAYER(4, s2, r.sl2)
+#undef D1_STAIR_LAYER
         if (want_monster) {
-            bool need = lane_alive(c) && in_view(x, x.mpos);
-            if (need && r.mlayer < 0 && bit(sm->reach, x.mpos)) r.mlayer = layer;
-            if (ballot(need && r.mlayer < 0)) done = false;
+            if (ballot(mneed && r.mlayer < 0)) {
+                const Row q0 = {(uint32_t)__shfl((int)r0.a, msrc), (uint32_t)__shfl((int)r0.b, msrc), (uint32_t)__shfl((int)r0.c, msrc)};
+                const Row q1 = {(uint32_t)__shfl((int)r1.a, msrc), (uint32_t)__shfl((int)r1.b, msrc), (uint32_t)__shfl((int)r1.c, msrc)};
+                const uint32_t w = row_word(my >= 64 ? q1 : q0, mword);
+                if (mneed && r.mlayer < 0 && (w & mbit)) r.mlayer = layer;
+                if (ballot(mneed && r.mlayer < 0)) done = false;
+            }
         }
         if (done) break;
     }
-    if (want_anchor && r.alayer < 0) {   // no reachable anchor: the anchor set is not needed
-        for (int w = x.lane; w < ROWS_WORDS; w += 64) L->anch[w] = 0;
-        __syncthreads();
+    row_st(sm->reach, lane, r0);
+    row_st(sm->front, lane, f0);
+    if (has1) { row_st(sm->reach, 64 + lane, r1); row_st(sm->front, 64 + lane, f1); }
+    if (want_anchor) {   // the nearest layer's anchors; none reachable: the set is not needed
+        row_st(L->anch, lane, r.alayer >= 0 ? a0 : zero);
+        if (has1) row_st(L->anch, 64 + lane, r.alayer >= 0 ? a1 : zero);
     }
+    __syncthreads();
     return r;
 }
 // route_first_step (learn.cu:248-264): back from target (at layer D) along the first
@@ -931,7 +964,7 @@ __global__ __launch_bounds__(64) void k_learn_init(uint8_t *state, int n, D1Conf
     observe_learn(c, obs ? obs + (size_t)env * D1L_OBS : nullptr, mask ? mask + (size_t)env * D1L_ACTIONS : nullptr);
 }
 template <int CLUMP>
-__global__ __launch_bounds__(64) void k_learn_step(uint8_t *state, int n, D1Config cfg, D1LTables t,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_learn_step(uint8_t *state, int n, D1Config cfg, D1LTables t,
                                                    const int64_t *actions, int limit, float *obs, float *mask,
                                                    float *out, const bool *active) {
     __shared__ LSmem L;
