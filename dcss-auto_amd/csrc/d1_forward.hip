@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
             }
     };
     // stage W2 + head (contiguous in the packed buffer) into LDS in 3 rounds of 12 pieces;
-    // the h1 conversion runs while the first round is in flight
+    // the h1 conversion runs while the first two rounds are in flight
     {
         constexpr int RND = NSTAGE / 256 / 3;
         u32x4 v[RND];
@@ -248,11 +248,14 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
 #pragma unroll
             for (int i = 0; i < RND; i++) stage[t + 256 * (RND * r + i)] = v[i];
         };
+        u32x4 v1[RND];   // the second round is in flight with the first
         sload(0);
+#pragma unroll
+        for (int i = 0; i < RND; i++) v1[i] = *(const u32x4 *)(wpk + PW2 + (size_t)(t + 256 * (RND + i)) * 8);
         to_frags(bl);
         sstore(0);
-        sload(1);
-        sstore(1);
+#pragma unroll
+        for (int i = 0; i < RND; i++) stage[t + 256 * (RND + i)] = v1[i];
         sload(2);
         sstore(2);
     }
