@@ -315,14 +315,27 @@ __device__ __forceinline__ uint64_t opaque_set(const Ctx &x, int ox, int oy, int
 }
 // Player field of view: vis_q bit j set when target (j%8, j/8) of quadrant q is in
 // bounds and one of its rays misses every opaque blocker.
+// The ray slots are loaded four at a time, the next four in flight while the current ones
+// are tested (past the last slot the loads repeat it, which changes no test): one load per
+// slot, each waited for before the next, left the whole view waiting on 11 serial latencies.
 __device__ __forceinline__ void compute_view(Ctx &x) {
     int px = x.player % W, py = x.player / W;
+    const int ns = x.nslots;
+    uint64_t m[4] = {0, 0, 0, 0};
+    auto load4 = [&](int s0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) m[i] = x.rays[imin(s0 + i, ns - 1) * 64 + x.lane];
+    };
+    if (ns > 0) load4(0);   // in flight during the opaque-set reads
     uint64_t o0 = opaque_set(x, px, py, 0), o1 = opaque_set(x, px, py, 1);
     uint64_t o2 = opaque_set(x, px, py, 2), o3 = opaque_set(x, px, py, 3);
     bool a0 = false, a1 = false, a2 = false, a3 = false;
-    for (int s = 0; s < x.nslots; s++) {
-        uint64_t m = x.rays[s * 64 + x.lane];
-        a0 |= (m & o0) == 0; a1 |= (m & o1) == 0; a2 |= (m & o2) == 0; a3 |= (m & o3) == 0;
+    for (int s0 = 0; s0 < ns; s0 += 4) {
+        const uint64_t c0 = m[0], c1 = m[1], c2 = m[2], c3 = m[3];
+        if (s0 + 4 < ns) load4(s0 + 4);
+#define D1_RAY_TEST(v) a0 |= ((v) & o0) == 0; a1 |= ((v) & o1) == 0; a2 |= ((v) & o2) == 0; a3 |= ((v) & o3) == 0;
+        D1_RAY_TEST(c0) D1_RAY_TEST(c1) D1_RAY_TEST(c2) D1_RAY_TEST(c3)
+#undef D1_RAY_TEST
     }
     int tx = x.lane & 7, ty = x.lane >> 3;
     x.vis0 = ballot(a0 && inb(px + tx, py + ty));
@@ -337,12 +350,14 @@ __device__ __forceinline__ bool detects(Ctx &x, int origin) {
     if (iabs(dx) > 6 || iabs(dy) > 6) return false;
     if (!x.c->wake_los) return true;
     int t = iabs(dy) * 8 + iabs(dx);
+    const bool has = x.lane < x.nslots;
+    const uint64_t ray = has ? x.rays[x.lane * 64 + t] : 0;   // the same slot for every quadrant
     bool det = false;
     for (int q = 0; q < 4; q++) {
         bool sx = q_sx(q), sy = q_sy(q);
         if ((dx && (dx > 0) != sx) || (dy && (dy > 0) != sy)) continue;
         uint64_t opq = opaque_set(x, ox, oy, q);
-        bool alive = x.lane < x.nslots && (x.rays[imin(x.lane, x.nslots - 1) * 64 + t] & opq) == 0;
+        bool alive = has && (ray & opq) == 0;
         det |= ballot(alive) != 0;
     }
     return det;
