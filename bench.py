@@ -165,6 +165,7 @@ def panel_bench(args):
                                     'limit': 2048}}
 
 
+EVERY = 8   # timed steps per sampled set of per-kernel events
 REFERENCE_WAITS_PER_S = 10.165e6   # gpu-d1/RESULTS.md:16, warp per world, RTX 5000 Max-Q
 
 
@@ -267,18 +268,22 @@ def learn_bench(args, warmup=8):
     for _ in range(warmup):
         env.step(env.heuristic())
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, EVERY)]
     t0 = time.perf_counter()
-    for k in range(args.steps):
-        ev[k][0].record()
+    for k in range(args.steps):   # per-kernel events on every EVERY-th decision, as in the rollout
+        e = ev[k // EVERY] if k % EVERY == 0 else None
+        if e is not None:
+            e[0].record()
         a = env.heuristic()
-        ev[k][1].record()
+        if e is not None:
+            e[1].record()
         env.step(a)
-        ev[k][2].record()
+        if e is not None:
+            e[2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    heur_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    step_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    heur_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev)
+    step_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev)
     achieved = LEARN_STEP_BYTES * n / (step_ms * 1e-3) / 1e9
     result = {'metric': 'learning-task decisions/s (d1-stairs-v2 learn_* drop-in, controller actions)',
               'value': n * args.steps / wall, 'unit': 'decisions/s', 'n_gpus': 1, 'steps': args.steps,
@@ -289,7 +294,8 @@ def learn_bench(args, warmup=8):
               'roofline': {'bound': 'hbm', 'kernel': 'd1::learn::k_learn_step', 'achieved': achieved,
                            'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS,
                            'traffic': measured_traffic(ROOT / 'profiles' / 'k_learn_step_learn.md'),
-                           'bytes_per_env_step': LEARN_STEP_BYTES, 'avg_launch_ms': step_ms},
+                           'bytes_per_env_step': LEARN_STEP_BYTES, 'avg_launch_ms': step_ms,
+                           'timed_launches': len(ev)},
               'heuristic_ms': heur_ms, 'step_ms': step_ms,
               'errors': int(env.errors().numel())}
     if not args.no_cpu_baseline:
@@ -376,14 +382,17 @@ def main():
     for t in range(args.warmup):
         one_step(t)
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # per-kernel HIP events on every EVERY-th step of the timed region: an event record costs
+    # the stream a few microseconds, so events around every launch would slow the
+    # throughput being measured (three per step: ~4%)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, EVERY)]
     t0 = time.perf_counter()
     for k in range(args.steps):
-        one_step(args.warmup + k, events[k])
+        one_step(args.warmup + k, events[k // EVERY] if k % EVERY == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
-    trunk_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
+    trunk_ms = sum(e[1].elapsed_time(e[2]) for e in events) / len(events)
     decisions = n * args.steps / wall
     step_bytes = STEP_BYTES.get(args.monsters, 3270)
     achieved = step_bytes * n / (step_ms * 1e-3) / 1e9
@@ -406,7 +415,8 @@ def main():
                    'rollout_steps': args.steps},
         'roofline': {'bound': 'hbm', 'kernel': 'd1::k_step', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
                      'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': measured_traffic(),
-                     'bytes_per_env_step': step_bytes, 'avg_launch_ms': step_ms},
+                     'bytes_per_env_step': step_bytes, 'avg_launch_ms': step_ms,
+                     'timed_launches': len(events)},
         'trunk': {'bound': 'mfma', 'achieved': trunk_tflops, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                   'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms},
     }
