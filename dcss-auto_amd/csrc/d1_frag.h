@@ -41,10 +41,10 @@ __device__ __forceinline__ uint16_t rb_num(float f) {
     return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 // two bytes of x (at bit 8s) -> two bf16 in one dword (exact: byte values need 8 bits)
-__device__ __forceinline__ uint32_t widen2(uint32_t x, int s) {
-    uint32_t lo = __float_as_uint((float)((x >> (8 * s)) & 255u)) >> 16;
-    uint32_t hi = __float_as_uint((float)((x >> (8 * s + 8)) & 255u)) & 0xFFFF0000u;
-    return lo | hi;
+__device__ __forceinline__ uint32_t widen2(uint32_t x, int s) {   // one v_perm pairs the high halves
+    const uint32_t lo = __float_as_uint((float)((x >> (8 * s)) & 255u));
+    const uint32_t hi = __float_as_uint((float)((x >> (8 * s + 8)) & 255u));
+    return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
 }
 // four bytes -> four bf16 (exact): the high halves of the converted floats, paired by v_perm
 // two floats -> two bf16 in one dword (lo in bits 0-15) with the hardware pack
