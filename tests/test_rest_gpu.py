@@ -1,0 +1,51 @@
+"""REST is repeated WAITs (the property the reference's own semantic self-test asserts for
+its macro, gpu-d1/branches/semantic-actions-v1/src/semantic_tests.cu:12-45, and that the
+d1-stairs-v2 transition keeps, branches/d1-stairs-v2/src/learn.cu:853-875): one REST
+decision leaves every world, RNG included, exactly where WAITs repeated as many turns
+leave it, and its reward is their rewards summed in order. Checked on the HIP library
+against itself with the reference's PCG stream (per-draw sequence), independent of the
+oracle. Only the decision and counter-step fields differ (one decision vs k)."""
+import importlib
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+T_OFF, DEC_OFF, TICKS_OFF = 20, 44, 36   # header: u32 t, i32 decisions, i32 ticks
+
+
+def i32(state, off):
+    return state[:, off:off + 4].contiguous().view(torch.int32)[:, 0]
+
+
+def test_rest_equals_repeated_waits(pkg):
+    print('[rest] REST vs WAITs', flush=True)
+    n = 2048
+    env = pkg.Env(n, pkg.reference_config(24), seed=21, hash=False)
+    g = torch.Generator().manual_seed(4)
+    for _ in range(80):   # moves, attacks and waits: players get hurt, monsters wake
+        env.step(torch.randint(0, 17, (n,), generator=g).cuda())
+    before = env.state.clone()
+    _, out = env.step(torch.full((n,), 17, dtype=torch.int64, device='cuda'))
+    rest_state, rest_out = env.state.clone(), out.clone()
+    done = rest_out[:, 1] > 0
+    k = i32(rest_state, TICKS_OFF) - i32(before, TICKS_OFF)   # turns the decision took
+    live = ~done
+    assert bool((k[live] >= 1).all())
+    assert int((k[live] > 1).sum()) >= 20, 'too few real rests to test'
+    env.state.copy_(before)
+    total = torch.zeros(n, device='cuda')
+    wait = torch.full((n,), 16, dtype=torch.int64, device='cuda')
+    for i in range(int(k[live].max())):
+        act = live & (k > i)
+        _, o = env.step(wait, active=act)
+        total = torch.where(act, total + o[:, 0], total)   # fp32, in turn order, as the macro sums
+    torch.cuda.synchronize()
+    a, b = rest_state[live].clone(), env.state[live].clone()
+    assert torch.equal(i32(b, DEC_OFF) - i32(a, DEC_OFF), k[live] - 1)
+    for off in (T_OFF, DEC_OFF):   # the only fields allowed to differ
+        a[:, off:off + 4] = 0
+        b[:, off:off + 4] = 0
+    assert torch.equal(a, b)
+    assert torch.equal(total[live], rest_out[live, 0])
