@@ -49,3 +49,39 @@ def test_rest_equals_repeated_waits(pkg):
         b[:, off:off + 4] = 0
     assert torch.equal(a, b)
     assert torch.equal(total[live], rest_out[live, 0])
+
+
+def test_learning_task_rest_equals_repeated_waits():
+    """The same on the learn_* drop-in (d1-stairs-v2 task, map 1057, 24 enemies): state,
+    frontier list, observation and mask equal; out[0] and out[40] (undiscounted in this
+    task) are the summed rewards and out[26] the turn count."""
+    L = importlib.import_module('dcss-auto_amd.learn')
+    print('[rest] learning task', flush=True)
+    n = 2048
+    env = L.LearnEnv(n, seed=33, clump=0)
+    g = torch.Generator().manual_seed(6)
+    for _ in range(80):
+        env.step(torch.randint(0, 17, (n,), generator=g).cuda())
+    before = (env.state.clone(), env.obs.clone(), env.mask.clone())
+    _, out = env.step(torch.full((n,), 17, dtype=torch.int64, device='cuda'))
+    rest_state, rest_obs, rest_mask, rest_out = env.state.clone(), env.obs.clone(), env.mask.clone(), out.clone()
+    done = rest_out[:, 1] > 0
+    k = rest_out[:, 26].to(torch.int64)
+    live = ~done
+    assert bool((k[live] >= 1).all()) and int((k[live] > 1).sum()) >= 20, 'too few real rests to test'
+    env.state.copy_(before[0]); env.obs.copy_(before[1]); env.mask.copy_(before[2])
+    total = torch.zeros(n, device='cuda')
+    wait = torch.full((n,), 16, dtype=torch.int64, device='cuda')
+    for i in range(int(k[live].max())):
+        act = live & (k > i)
+        _, o = env.step(wait, active=act)
+        total = torch.where(act, total + o[:, 0], total)
+    torch.cuda.synchronize()
+    a, b = rest_state[live].clone(), env.state[live].clone()
+    DEC = 32   # learn header: i32 decisions
+    assert torch.equal(i32(b, DEC) - i32(a, DEC), k[live].to(torch.int32) - 1)
+    a[:, DEC:DEC + 4] = 0
+    b[:, DEC:DEC + 4] = 0
+    assert torch.equal(a, b)
+    assert torch.equal(env.obs[live], rest_obs[live]) and torch.equal(env.mask[live], rest_mask[live])
+    assert torch.equal(total[live], rest_out[live, 0]) and torch.equal(total[live], rest_out[live, 40])
