@@ -4,7 +4,8 @@ d1-stairs-v2 transition keeps, branches/d1-stairs-v2/src/learn.cu:853-875): one 
 decision leaves every world, RNG included, exactly where WAITs repeated as many turns
 leave it, and its reward is their rewards summed in order. Checked on the HIP library
 against itself with the reference's PCG stream (per-draw sequence), independent of the
-oracle. Only the decision and counter-step fields differ (one decision vs k)."""
+oracle. Only the decision and counter-step fields differ (one decision vs k). Also: an
+invalid decision is exactly one WAIT turn."""
 import importlib
 
 import pytest
@@ -85,3 +86,43 @@ def test_learning_task_rest_equals_repeated_waits():
     assert torch.equal(a, b)
     assert torch.equal(env.obs[live], rest_obs[live]) and torch.equal(env.mask[live], rest_mask[live])
     assert torch.equal(total[live], rest_out[live, 0]) and torch.equal(total[live], rest_out[live, 40])
+
+
+def test_invalid_actions_are_one_wait(pkg):
+    """An invalid decision degrades to one ordinary WAIT turn, not a zero-time transition
+    (the reference's semantic self-test, semantic_tests.cu:44): out-of-range codes on the
+    HIP env, and on the learning task every action its own mask marks invalid."""
+    print('[rest] invalid actions', flush=True)
+    n = 2048
+    env = pkg.Env(n, pkg.reference_config(24), seed=5, hash=False)
+    g = torch.Generator().manual_seed(8)
+    for _ in range(40):
+        env.step(torch.randint(0, 17, (n,), generator=g).cuda())
+    before = env.state.clone()
+    codes = torch.tensor([-1, 19, 50, 1000, 2000, -7], dtype=torch.int64)
+    bad = codes[torch.randint(0, len(codes), (n,), generator=g)].cuda()
+    _, o1 = env.step(bad)
+    s1, out1, obs1 = env.state.clone(), o1.clone(), env.obs.clone()
+    env.state.copy_(before)
+    _, o2 = env.step(torch.full((n,), 16, dtype=torch.int64, device='cuda'))
+    assert torch.equal(s1, env.state) and torch.equal(out1, o2) and torch.equal(obs1, env.obs)
+
+    L = importlib.import_module('dcss-auto_amd.learn')
+    lenv = L.LearnEnv(n, seed=9, clump=0)
+    for _ in range(40):
+        lenv.step(torch.randint(0, 17, (n,), generator=g).cuda())
+    masked = (lenv.mask[:, :19] == 0)
+    assert int(masked.any(1).sum()) > n // 2
+    pick = torch.where(masked, torch.rand(n, 19, device='cuda'), torch.full((n, 19), -1.0, device='cuda')).argmax(1)
+    acts = torch.where(masked.any(1), pick, torch.full_like(pick, 16)).contiguous()
+    before = (lenv.state.clone(), lenv.obs.clone(), lenv.mask.clone())
+    _, o1 = lenv.step(acts)
+    s1, out1, obs1, m1 = lenv.state.clone(), o1.clone(), lenv.obs.clone(), lenv.mask.clone()
+    lenv.state.copy_(before[0]); lenv.obs.copy_(before[1]); lenv.mask.copy_(before[2])
+    _, o2 = lenv.step(torch.full((n,), 16, dtype=torch.int64, device='cuda'))
+    assert torch.equal(s1, lenv.state) and torch.equal(obs1, lenv.obs) and torch.equal(m1, lenv.mask)
+    # the outcome rows agree except the REST statistics of worlds that asked for an invalid REST
+    keep = torch.ones(45, dtype=torch.bool, device='cuda')
+    keep[34:40] = False
+    assert torch.equal(out1[:, keep], o2[:, keep])
+    assert bool((out1[acts == 17, 38] == 1).all())   # flagged as an invalid REST
