@@ -41,22 +41,25 @@ def measured_traffic(path=ROOT / 'profiles' / 'k_step_hbm_traffic.md'):
     return None
 
 
-def cpu_baseline(envs=1024, steps=1000, threads=None):
+def cpu_baseline(envs=1024, steps=1000, runs=3, threads=None):
     """The CPU restatement (oracle/, OpenMP over worlds) on config C1: 1,024 generated
-    levels, 8 monsters, uniform random actions over 16, 1,000 steps."""
+    levels, 8 monsters, uniform random actions over 16, 1,000 steps; `runs` independent
+    runs (seeds 1, 2, ...) so that the sample is 10-20 s of CPU work."""
     import numpy as np
     from oracle import oracle as O
     pkg = importlib.import_module('dcss-auto_amd')
     threads = threads or min(16, os.cpu_count() or 1)
-    env = O.OracleEnv(envs, pkg.baseline_config(), seed=1, threads=threads)
-    actions = np.random.default_rng(2).integers(0, 16, (steps, envs)).astype(np.int64)
-    t0 = time.perf_counter()
-    for k in range(steps):
-        env.step(actions[k])
-    dt = time.perf_counter() - t0
-    return {'value': envs * steps / dt, 'unit': 'env decisions/s', 'cores': threads, 'kind': 'port',
-            'sample': f'C1 full: {envs} generated levels x {steps} steps, 8 monsters, random actions, '
-                      f'step+obs+hash, {dt:.2f} s wall'}
+    dt = 0.0
+    for r in range(runs):
+        env = O.OracleEnv(envs, pkg.baseline_config(), seed=1 + r, threads=threads)
+        actions = np.random.default_rng(2 + r).integers(0, 16, (steps, envs)).astype(np.int64)
+        t0 = time.perf_counter()
+        for k in range(steps):
+            env.step(actions[k])
+        dt += time.perf_counter() - t0
+    return {'value': runs * envs * steps / dt, 'unit': 'env decisions/s', 'cores': threads, 'kind': 'port',
+            'sample': f'C1 full, {runs} runs: {envs} generated levels x {steps} steps each, 8 monsters, '
+                      f'random actions, step+obs+hash, {dt:.2f} s wall on {threads} threads'}
 
 
 def ppo_bench(args, env, rollout_model, policy_mod, dev):
