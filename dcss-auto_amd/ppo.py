@@ -239,13 +239,15 @@ class FastPPO:
     def update(self, buf, generator=None):
         adv, ret = self.advantages(buf)
         n = buf.T * buf.N
+        obs, actions, logp = self._views(buf)
         if self.graph:
             if self._g is None or self._g_buf is not buf:
                 self._capture(buf)
             self._adv.copy_(adv)
             self._ret.copy_(ret)
             adv, ret = self._adv, self._ret
-        obs, actions, logp = self._views(buf)
+            if not self._packed:   # weights replaced outside the step (a checkpoint load): the graph
+                self._struct(obs, actions, logp, adv, ret)   # only replays, so rebuild its weight copies here
         steps = n // self.minibatch            # a ragged tail is dropped (T*N is a multiple in C4)
         for _ in range(self.epochs):
             self.set_order(torch.randperm(n, device=self.dev, generator=generator))

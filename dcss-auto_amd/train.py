@@ -44,6 +44,11 @@ class Trainer:
         self.buf = ppo_mod.RolloutBuffer(horizon, self.N, device=self.dev)
         self.seed = seed
         self.graph = graph
+        # everything besides the tensors that decides what the next update computes: a
+        # checkpoint made with other values would not resume the same run
+        self.hparams = dict(seed=seed, horizon=horizon, batch=self.N, minibatch=minibatch, epochs=epochs, lr=lr,
+                            eps=eps, clip=clip, vcoef=vcoef, ecoef=ecoef, max_grad_norm=max_grad_norm, gamma=gamma,
+                            lam=lam)
         self.next_obs = env.obs.reshape(self.N, -1).clone()       # the observation the next rollout starts from
         self.t_dev = torch.zeros(1, dtype=torch.int32, device=self.dev)   # sampler counter step
         self.logits = torch.empty((self.N, P.N_ACTIONS), dtype=torch.float32, device=self.dev)
@@ -157,10 +162,16 @@ class Trainer:
         cpu = lambda t: t.detach().to('cpu', copy=True)
         return dict(p=cpu(F.p), pb=cpu(F.pb), m=cpu(F.m), v=cpu(F.v), adam_step=cpu(self.ppo.step_t),
                     env_state=cpu(self.env.state), next_obs=cpu(self.next_obs), t=cpu(self.t_dev),
-                    gen=self.gen.get_state(), updates=torch.tensor(self.updates), decisions=torch.tensor(self.decisions))
+                    gen=self.gen.get_state(), updates=torch.tensor(self.updates), decisions=torch.tensor(self.decisions),
+                    hparams=dict(self.hparams))
 
     def load_state_dict(self, sd):
         F = self.ppo.flat
+        saved = sd.get('hparams')
+        if saved != self.hparams:
+            diff = sorted(k for k in set(self.hparams) | set(saved or {})
+                          if (saved or {}).get(k) != self.hparams.get(k))
+            raise ValueError(f'checkpoint was made with other trainer settings: {diff}')
         for dst, key in ((F.p, 'p'), (F.pb, 'pb'), (F.m, 'm'), (F.v, 'v'), (self.ppo.step_t, 'adam_step'),
                          (self.env.state, 'env_state'), (self.next_obs, 'next_obs'), (self.t_dev, 't')):
             if dst.shape != sd[key].shape or dst.dtype != sd[key].dtype:
@@ -168,7 +179,7 @@ class Trainer:
             dst.copy_(sd[key])
         self.gen.set_state(sd['gen'])
         self.updates, self.decisions = int(sd['updates']), int(sd['decisions'])
-        self.ppo._packed = False   # FastPPO's kernel-ordered weight copies are rebuilt from pb
+        self.ppo._packed = False   # FastPPO rebuilds its kernel-ordered weight copies from pb before its next step
         self._repack()
 
     def save(self, path):

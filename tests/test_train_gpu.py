@@ -19,6 +19,15 @@ def make_trainer(pkg, graph, n=2048, T=8, seed=11):
     return train.Trainer(env, model, horizon=T, minibatch=8192, epochs=2, graph=graph)
 
 
+def assert_same_state(a, b):
+    assert a.keys() == b.keys()
+    for key in a:
+        if key == 'hparams':
+            assert a[key] == b[key]
+        else:
+            assert torch.equal(a[key], b[key]), key
+
+
 def test_sample_dev_matches_sample():
     P = importlib.import_module('dcss-auto_amd.policy')
     print('[train] sample_dev', flush=True)
@@ -75,15 +84,54 @@ def test_resume_is_bit_exact(pkg, tmp_path):
     resumed.train(2)
     torch.cuda.synchronize()
     a, b = full.state_dict(), resumed.state_dict()
-    for key in a:
-        if key == 'gen':
-            assert torch.equal(a[key], b[key]), key
-        else:
-            assert torch.equal(a[key], b[key]), key
+    assert_same_state(a, b)
     assert int(a['updates']) == 4 and int(a['decisions']) == 4 * 8 * 2048
     # the weights moved, and sync_model writes them into the module
     model = resumed.sync_model()
     assert torch.equal(model.l1.weight.detach().reshape(-1), resumed.ppo.flat.view(resumed.ppo.flat.p, 'l1.weight').reshape(-1))
+
+
+def test_load_into_a_trained_graph_trainer(pkg, tmp_path):
+    """A graph-mode trainer that has already trained (its PPO graph captured, its packed
+    weight copies current) loads another run's checkpoint: the next updates equal those of
+    a fresh trainer resumed from the same checkpoint, bit for bit (the captured PPO graph
+    must not step on the pre-load weights)."""
+    print('[train] load into a trained trainer', flush=True)
+    src = make_trainer(pkg, graph=True)
+    src.train(2)
+    src.save(tmp_path / 'ckpt.pt')
+    busy = make_trainer(pkg, graph=True, seed=999)
+    busy.model.l1.weight.data.mul_(0.5)            # a different run: other weights, other worlds
+    busy.ppo.flat.p.mul_(0.5)
+    busy.ppo.flat.pb.copy_(busy.ppo.flat.p)
+    busy.ppo._packed = False
+    busy._repack()
+    busy.train(2)                                   # captures both graphs on the other weights
+    busy.load(tmp_path / 'ckpt.pt')
+    busy.train(2)
+    fresh = make_trainer(pkg, graph=True, seed=4321)
+    fresh.load(tmp_path / 'ckpt.pt')
+    fresh.train(2)
+    torch.cuda.synchronize()
+    assert_same_state(fresh.state_dict(), busy.state_dict())
+
+
+def test_checkpoint_refuses_other_settings(pkg, tmp_path):
+    """A checkpoint records the trainer settings that decide the next update (sampler seed,
+    horizon, batch, minibatch, epochs, optimiser and loss coefficients); loading it into a
+    trainer built with other settings raises instead of silently diverging."""
+    print('[train] checkpoint settings', flush=True)
+    train = importlib.import_module('dcss-auto_amd.train')
+    P = importlib.import_module('dcss-auto_amd.policy')
+    src = make_trainer(pkg, graph=False)
+    src.save(tmp_path / 'ckpt.pt')
+    env = pkg.Env(2048, pkg.baseline_config(8), seed=11, hash=False)
+    other = train.Trainer(env, P.Policy(seed=2).cuda(), horizon=8, minibatch=8192, epochs=2, graph=False, lr=1e-3)
+    with pytest.raises(ValueError, match='lr'):
+        other.load(tmp_path / 'ckpt.pt')
+    reseeded = train.Trainer(env, P.Policy(seed=2).cuda(), horizon=8, minibatch=8192, epochs=2, graph=False, seed=8)
+    with pytest.raises(ValueError, match='seed'):
+        reseeded.load(tmp_path / 'ckpt.pt')
 
 
 def test_evaluation_ends_every_episode(pkg):
@@ -161,6 +209,4 @@ def test_worker_loop_stop_and_resume_is_bit_exact(pkg, tmp_path):
     resumed = make_trainer(pkg, graph=True, seed=12345)
     assert resumed.run(target, checkpoint=ck) == 0
     torch.cuda.synchronize()
-    a, b = full.state_dict(), resumed.state_dict()
-    for key in a:
-        assert torch.equal(a[key], b[key]), key
+    assert_same_state(full.state_dict(), resumed.state_dict())
