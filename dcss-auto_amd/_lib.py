@@ -10,7 +10,7 @@ _LIB = None
 
 SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
            'd1_init', 'd1_step', 'd1_sample', 'd1_sample_dev', 'd1_gae', 'd1_obs_to_bf16', 'd1_obs_d4',
-           'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
+           'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step', 'd1_ppo_step_static', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
            'd1_sample_ar', 'd1_los_table', 'd1_distance_rows', 'd1_policy_packed_elems', 'd1_policy_pack',
            'd1_policy_fwd', 'd1_policy_fwd_sample')
 LEARN_SYMBOLS = ('learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size',
@@ -53,6 +53,7 @@ def load():
         L.d1_ppo_work_bytes.restype = C.c_int64
         L.d1_ppo_step.argtypes = [C.POINTER(D1PPOStep), p]
         L.d1_ppo_prepare.argtypes = [C.POINTER(D1PPOStep), p]
+        L.d1_ppo_step_static.argtypes = [C.POINTER(D1PPOStep), p]
         L.d1_sample_ar.argtypes = [p, i, i, p, i, i, i, C.c_uint64, C.c_uint32, p, p, p, p, p]
         L.d1_wait_bytes.argtypes = []
         L.d1_wait_init.argtypes = [p, i, i, p, p, C.c_uint64, i, p]

@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/d1hip.h"
 #include "d1_frag.h"
 
@@ -780,38 +782,35 @@ __global__ __launch_bounds__(256) void k_pack(D1PPOStep a, uint16_t *wpk) {
 struct Layout {
     size_t wpk, h1f, h2f, dh2f, dh1f, dzf, xf, bpart, part1, part2, part3, npart, total;
 };
-static Layout layout(int mb) {
+constexpr size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+constexpr Layout layout(int mb) {
     Layout L{};
     size_t off = 0;
-    auto take = [&](size_t bytes) {
-        const size_t at = off;
-        off += (bytes + 255) / 256 * 256;
-        return at;
-    };
-    L.wpk = take((size_t)P_END * 2);
-    L.h1f = take((size_t)H * mb * 2);
-    L.h2f = take((size_t)H * mb * 2);
-    L.dh2f = take((size_t)H * mb * 2);
-    L.dh1f = take((size_t)H * mb * 2);
-    L.dzf = take((size_t)32 * mb * 2);
-    L.xf = take((size_t)XB * 32 * mb);
-    L.bpart = take((size_t)(mb / R) * BP * 4);
-    L.part1 = take((size_t)(mb / KW) * H * K1 * 4);
-    L.part2 = take((size_t)(mb / KW) * H * H * 4);
-    L.part3 = take((size_t)(mb / KW2) * NZ * H * 4);
-    L.npart = take((size_t)(NRED + NBIASB) * 4);
+    L.wpk = off, off += round256((size_t)P_END * 2);
+    L.h1f = off, off += round256((size_t)H * mb * 2);
+    L.h2f = off, off += round256((size_t)H * mb * 2);
+    L.dh2f = off, off += round256((size_t)H * mb * 2);
+    L.dh1f = off, off += round256((size_t)H * mb * 2);
+    L.dzf = off, off += round256((size_t)32 * mb * 2);
+    L.xf = off, off += round256((size_t)XB * 32 * mb);
+    L.bpart = off, off += round256((size_t)(mb / R) * BP * 4);
+    L.part1 = off, off += round256((size_t)(mb / KW) * H * K1 * 4);
+    L.part2 = off, off += round256((size_t)(mb / KW) * H * H * 4);
+    L.part3 = off, off += round256((size_t)(mb / KW2) * NZ * H * 4);
+    L.npart = off, off += round256((size_t)(NRED + NBIASB) * 4);
     L.total = off;
     return L;
 }
 
-static int check_args(const D1PPOStep *s, Work *w) {
+// Validates everything but the work buffer; `base`/`bytes` is the work buffer to carve.
+static int check_args(const D1PPOStep *s, char *base, int64_t bytes, Work *w) {
     if (!s) return D1_E_ARG;
     const D1PPOStep &a = *s;
     if (a.mb <= 0 || a.mb % KW || a.n < a.mb || a.n >= ((int64_t)1 << 31) || a.nparams % 4) return D1_E_ARG;
     if (!a.obs || !a.perm || !a.cursor || !a.actions || !a.logp_old || !a.adv || !a.ret || !a.p || !a.pb || !a.g ||
-        !a.m || !a.v || !a.step || !a.loss_parts || !a.work)
+        !a.m || !a.v || !a.step || !a.loss_parts || !base)
         return D1_E_ARG;
-    if ((uintptr_t)a.obs % 8 || (uintptr_t)a.pb % 16 || (uintptr_t)a.g % 16 || (uintptr_t)a.work % 256 ||
+    if ((uintptr_t)a.obs % 8 || (uintptr_t)a.pb % 16 || (uintptr_t)a.g % 16 || (uintptr_t)base % 256 ||
         (uintptr_t)a.p % 16 || (uintptr_t)a.m % 16 || (uintptr_t)a.v % 16)
         return D1_E_ARG;
     const int64_t offs[6] = {a.off_w1, a.off_b1, a.off_w2, a.off_b2, a.off_w3, a.off_b3};
@@ -819,8 +818,7 @@ static int check_args(const D1PPOStep *s, Work *w) {
     for (int i = 0; i < 6; i++)
         if (offs[i] < 0 || offs[i] % 8 || offs[i] + sizes[i] > a.nparams) return D1_E_ARG;
     const Layout L = layout(a.mb);
-    if (a.work_bytes < (int64_t)L.total) return D1_E_ARG;
-    char *base = (char *)a.work;
+    if (bytes < (int64_t)L.total) return D1_E_ARG;
     w->wpk = (uint16_t *)(base + L.wpk);
     w->h1f = (uint16_t *)(base + L.h1f);
     w->h2f = (uint16_t *)(base + L.h2f);
@@ -835,6 +833,55 @@ static int check_args(const D1PPOStep *s, Work *w) {
     w->npart = (float *)(base + L.npart);
     return 0;
 }
+static int check_args(const D1PPOStep *s, Work *w) {
+    if (!s) return D1_E_ARG;
+    return check_args(s, (char *)s->work, s->work_bytes, w);
+}
+
+static void launch_pack(const D1PPOStep &a, const Work &w, hipStream_t st) {
+    hipLaunchKernelGGL(k_pack_zero, dim3(256), dim3(256), 0, st, w.wpk);
+    hipLaunchKernelGGL(k_pack, dim3(512), dim3(256), 0, st, a, w.wpk);
+}
+static void launch_step(const D1PPOStep &a, const Work &w, hipStream_t st) {
+    const int s1 = a.mb / KW, s2 = a.mb / KW2;
+    hipLaunchKernelGGL(k_rows, dim3(a.mb / R), dim3(512), 0, st, a, w);
+    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1 + s2), dim3(256), 0, st, a, w);
+    hipLaunchKernelGGL(k_reduce, dim3(NRED + NBIASB), dim3(256), 0, st, a, w);
+    const int64_t nadam = (a.nparams / 4 + 255) / 256;   // one group of four parameters per lane
+    hipLaunchKernelGGL(k_adam, dim3((unsigned)nadam), dim3(256), 0, st, a, w);
+}
+
+// ---------------------------------------------------------------- library-owned work buffer
+// d1_ppo_step_static's work buffer: one per GPU, held from the first use until the process
+// ends, sized for the largest minibatch it accepts. In host code `scratch` names a host-side
+// stand-in, never the device array: the device address comes from hipGetSymbolAddress, once
+// per device, with that device current.
+constexpr size_t SCRATCH_BYTES = layout(D1_PPO_STATIC_MAX_MB).total;
+static __device__ __align__(256) char scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex scratch_lock;
+static char *scratch_ptr[MAX_DEVICES];
+
+// The device address of this device's `scratch`, or null with *err set.
+static char *scratch_base(int *err) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        *err = D1_E_ARG;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (!scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            *err = e != hipSuccess ? (int)e : D1_E_ARG;
+            return nullptr;
+        }
+        scratch_ptr[dev] = (char *)ptr;
+    }
+    return scratch_ptr[dev];
+}
 
 }  // namespace d1q
 
@@ -847,9 +894,7 @@ extern "C" int d1_ppo_prepare(const D1PPOStep *s, void *stream) {
     using namespace d1q;
     Work w;
     if (int e = check_args(s, &w)) return e;
-    hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_pack_zero, dim3(256), dim3(256), 0, st, w.wpk);
-    hipLaunchKernelGGL(k_pack, dim3(512), dim3(256), 0, st, *s, w.wpk);
+    launch_pack(*s, w, (hipStream_t)stream);
     return (int)hipGetLastError();
 }
 
@@ -857,13 +902,21 @@ extern "C" int d1_ppo_step(const D1PPOStep *s, void *stream) {
     using namespace d1q;
     Work w;
     if (int e = check_args(s, &w)) return e;
-    const D1PPOStep &a = *s;
-    const int s1 = a.mb / KW, s2 = a.mb / KW2;
-    hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_rows, dim3(a.mb / R), dim3(512), 0, st, a, w);
-    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1 + s2), dim3(256), 0, st, a, w);
-    hipLaunchKernelGGL(k_reduce, dim3(NRED + NBIASB), dim3(256), 0, st, a, w);
-    const int64_t nadam = (a.nparams / 4 + 255) / 256;   // one group of four parameters per lane
-    hipLaunchKernelGGL(k_adam, dim3((unsigned)nadam), dim3(256), 0, st, a, w);
+    launch_step(*s, w, (hipStream_t)stream);
+    return (int)hipGetLastError();
+}
+
+extern "C" int d1_ppo_step_static(const D1PPOStep *s, void *stream) {
+    using namespace d1q;
+    if (!s) return D1_E_ARG;
+    if (s->mb > D1_PPO_STATIC_MAX_MB) return D1_E_SCRATCH;
+    int err = 0;
+    char *base = scratch_base(&err);
+    if (!base) return err;
+    Work w;
+    if (int e = check_args(s, base, (int64_t)SCRATCH_BYTES, &w)) return e;
+    const hipStream_t st = (hipStream_t)stream;
+    launch_pack(*s, w, st);   // the packed weight copies are rebuilt from pb on every call
+    launch_step(*s, w, st);
     return (int)hipGetLastError();
 }

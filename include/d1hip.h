@@ -21,7 +21,8 @@
  * copied by value into the launch. Calls are asynchronous on `stream` (a
  * hipStream_t; 0 = the null stream). Return value: 0 on success, a hipError_t
  * code for launch failures, or a negative D1_E* code for rejected arguments.
- * The library allocates no memory and keeps no global state.
+ * The library allocates no memory; its only global state is the device work buffer
+ * that d1_ppo_step_static owns (one per GPU, see there).
  */
 #ifndef D1HIP_H
 #define D1HIP_H
@@ -244,6 +245,21 @@ typedef struct {
 int64_t d1_ppo_work_bytes(int mb);
 int d1_ppo_prepare(const D1PPOStep *s, void *stream);
 int d1_ppo_step(const D1PPOStep *s, void *stream);
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under graph capture, tight serving loops, harnesses that forbid hipMalloc): d1_ppo_step
+ * with the work buffer owned by the library, so s->work and s->work_bytes are ignored.
+ * The buffer is one file-scope device array per GPU of d1_ppo_work_bytes(D1_PPO_STATIC_MAX_MB)
+ * bytes (51,169,792), held from the library's load until the process ends; a larger s->mb
+ * returns D1_E_SCRATCH. Each call first rebuilds the packed
+ * weight copies from s->pb (as d1_ppo_prepare does) and then runs d1_ppo_step's kernels, so
+ * one call equals d1_ppo_prepare + d1_ppo_step on a private work buffer, bit for bit.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (two streams, two threads) race and give undefined results; calls in stream order do not.
+ * The call itself allocates nothing (no hipMalloc, no library allocation). */
+#define D1_PPO_STATIC_MAX_MB 8192
+#define D1_E_SCRATCH (-4)             /* request larger than the library-owned buffer */
+int d1_ppo_step_static(const D1PPOStep *s, void *stream);
 
 /* Reverse-time GAE over a [T, n] rollout (gpu-d1/scripts/run_ring_ablations.py:354-360):
  *   live = 1 - done[t]; delta = reward[t] + (gamma*next)*live - value[t];

@@ -17,6 +17,7 @@ def test_header_declares_the_abi():
     assert declared_symbols() == sorted(['d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size',
                                          'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_sample_dev', 'd1_gae',
                                          'd1_obs_to_bf16', 'd1_obs_d4', 'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step',
+                                         'd1_ppo_step_static',
                                          'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
                                          'd1_sample_ar', 'd1_los_table', 'd1_distance_rows', 'd1_policy_packed_elems',
                                          'd1_policy_pack', 'd1_policy_fwd', 'd1_policy_fwd_sample'])
