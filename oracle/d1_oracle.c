@@ -336,29 +336,97 @@ static void reset(OState *s, const D1Config *c) {
     reveal(s); /* the initial view earns no reward */
 }
 
-/* gpu-d1/src/sim.h:130-163 */
-static void attack(OState *s, const D1Config *c, int id) {
-    ORng *r = &s->rng;
-    const D1Kind *k = kind_of(s, c, id);
-    int hit = rng_r(r, k->tohit + 1);
-    int ev = rng_round(r, c->ev100, 100);
+/* ------------------------------------------------------------------ monster rules (shared) */
+static int m_kind(const OMonsters *m, int id, int field) {
+    return m->kinds[4 * (m->kind_of ? m->kind_of[id] : id % 6) + field];
+}
+/* gpu-d1/src/sim.h:130-163: to-hit against EV (probabilistically rounded, averaged),
+ * 5% automatic hit or miss, shield block against bypass while blocks < limit, damage
+ * 1 + r(damage) minus max(r(ac + 1), min(gdr * damage / 100, ac rounded by halves)) with
+ * the GDR table entry of a second, independent AC rounding. */
+void o_m_attack(OMonsters *m, int id) {
+    ORng *r = m->rng;
+    int hit = rng_r(r, m_kind(m, id, 2) + 1);
+    int ev = rng_round(r, m->ev100, 100);
     ev = rng_avg(r, 2 * ev);
     int margin = hit - ev;
     if (rng_r(r, 100) < 5) margin = (rng_r(r, 2) ? 1 : -1) * 1000;
-    int bypass = rng_r(r, k->bypass);
-    int sh = rng_round(r, c->sh100, 100);
+    int bypass = rng_r(r, m_kind(m, id, 3));
+    int sh = rng_round(r, m->sh100, 100);
     int block = rng_avg(r, sh * 2) / 3 - 1;
-    if (block >= bypass && s->blocks < c->shield_limit) { s->blocks++; return; }
+    if (block >= bypass && *m->blocks < m->shield_limit) { (*m->blocks)++; return; }
     if (margin < 0) return;
-    int damage = 1 + rng_r(r, k->damage);
-    int ac = rng_round(r, c->ac100, 100);
-    int gac = rng_round(r, c->ac100, 100);
-    int gdr = c->gdr[gac - c->ac100 / 100];
+    int dmg = m_kind(m, id, 1);
+    int damage = 1 + rng_r(r, dmg);
+    int ac = rng_round(r, m->ac100, 100);
+    int gac = rng_round(r, m->ac100, 100);
+    int gdr = gac - m->ac100 / 100 ? m->gdr1 : m->gdr0;
     int saved = rng_r(r, ac + 1);
     int half = rng_round(r, ac, 2);
-    saved = imax(saved, imin(gdr * k->damage / 100, half));
-    damage = imax(0, damage - saved);
-    s->hp -= damage;
+    saved = imax(saved, imin(gdr * dmg / 100, half));
+    *m->hp -= imax(0, damage - saved);
+}
+static int m_passable(const OMonsters *m, int q) {
+    return q >= 0 && m->floor[q] && q != m->player && m->occ[q] < 0;
+}
+/* gpu-d1/src/sim.h:207-253: greedy descent of the distance field, cardinals then
+ * diagonals from a rotation r(4); equal improvements replace the choice with probability
+ * 1/ties; when stuck (and repair is on), the first step of a 24-node breadth-first search
+ * towards any lower-distance cell. */
+int o_m_choose_move(OMonsters *m, const uint16_t *dist, int id) {
+    int p = m->pos[id], best = -1, bd = dist[p], ties = 0, rotation = rng_r(m->rng, 4);
+    for (int z = 0; z < 8; z++) {
+        int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
+        int q = neighbor(p, d);
+        if (!m_passable(m, q)) continue;
+        int dd = dist[q];
+        if (dd < bd) { bd = dd; best = q; ties = 1; }
+        else if (dd == bd && best >= 0 && rng_r(m->rng, ++ties) == 0) best = q;
+    }
+    if (best >= 0 || !m->repair) return best;
+    int cells[24], first[24], len = 1;
+    cells[0] = p;
+    first[0] = -1;
+    for (int head = 0; head < len; head++)
+        for (int d = 0; d < 8; d++) {
+            int q = neighbor(cells[head], d);
+            if (!m_passable(m, q)) continue;
+            int seen = 0;
+            for (int j = 0; j < len; j++) if (cells[j] == q) { seen = 1; break; }
+            if (seen) continue;
+            int step = head == 0 ? q : first[head];
+            if (dist[q] < dist[p]) return step;
+            if (len < 24) { cells[len] = q; first[len] = step; len++; }
+        }
+    return -1;
+}
+/* gpu-d1/src/sim.h:165-174: the next actor is the monster with the most energy >= 80,
+ * ties to the lowest id (the heap of :175-200 picks the same one). */
+int o_m_scan(const int16_t *energy, int count) {
+    int best = -1;
+    for (int i = 0; i < count; i++)
+        if (energy[i] >= 80 && (best < 0 || energy[i] > energy[best] || (energy[i] == energy[best] && i < best)))
+            best = i;
+    return best;
+}
+/* gpu-d1/src/sim.h:254-269: pay 10 energy, then melee when adjacent, else move (`dist`
+ * is read only for a move). */
+void o_m_act(OMonsters *m, const uint16_t *dist, int id) {
+    m->energy[id] = (int16_t)(m->energy[id] - 10);
+    if (cheb(m->pos[id], m->player) == 1) { o_m_attack(m, id); return; }
+    int q = o_m_choose_move(m, dist, id);
+    if (q >= 0) {
+        m->occ[m->pos[id]] = -1;
+        m->pos[id] = (int16_t)q;
+        m->occ[q] = (int16_t)id;
+    }
+}
+/* the env world's view */
+static OMonsters env_monsters(OState *s, const D1Config *c) {
+    OMonsters m = {&s->rng, &s->hp, &s->blocks, s->pos, s->energy, s->occ, s->floor, s->kind,
+                   (const int32_t *)c->kinds, s->player, c->ac100, c->ev100, c->sh100, c->shield_limit,
+                   c->repair, c->gdr[0], c->gdr[1]};
+    return m;
 }
 /* Distance-from-player field over floor, 8-neighbour BFS (what the reference's
  * all-pairs table rows hold, gpu-d1/scripts/learn_env.py:31-39). */
@@ -374,54 +442,6 @@ static void player_field(const OState *s, uint16_t *ds) {
             int q = neighbor(p, d);
             if (q >= 0 && s->floor[q] && ds[q] == 65535) { ds[q] = (uint16_t)(ds[p] + 1); queue[tail++] = (int16_t)q; }
         }
-    }
-}
-/* gpu-d1/src/sim.h:207-253 */
-static int choose_move(OState *s, const D1Config *c, const uint16_t *dist, int id) {
-    int p = s->pos[id], best = -1, bd = dist[p], ties = 0, rotation = rng_r(&s->rng, 4);
-    for (int z = 0; z < 8; z++) {
-        int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
-        int q = neighbor(p, d);
-        if (q < 0 || !s->floor[q] || q == s->player || s->occ[q] >= 0) continue;
-        int dd = dist[q];
-        if (dd < bd) { bd = dd; best = q; ties = 1; }
-        else if (dd == bd && best >= 0 && rng_r(&s->rng, ++ties) == 0) best = q;
-    }
-    if (best >= 0 || !c->repair) return best;
-    int cells[24], first[24], len = 1;
-    cells[0] = p;
-    first[0] = -1;
-    for (int head = 0; head < len; head++)
-        for (int d = 0; d < 8; d++) {
-            int q = neighbor(cells[head], d);
-            if (q < 0 || !s->floor[q] || q == s->player || s->occ[q] >= 0) continue;
-            int seen = 0;
-            for (int j = 0; j < len; j++) if (cells[j] == q) { seen = 1; break; }
-            if (seen) continue;
-            int step = head == 0 ? q : first[head];
-            if (dist[q] < dist[p]) return step;
-            if (len < 24) { cells[len] = q; first[len] = step; len++; }
-        }
-    return -1;
-}
-/* gpu-d1/src/sim.h:165-174 */
-static int scan(const OState *s, int count) {
-    int best = -1;
-    for (int i = 0; i < count; i++)
-        if (s->energy[i] >= 80 &&
-            (best < 0 || s->energy[i] > s->energy[best] || (s->energy[i] == s->energy[best] && i < best)))
-            best = i;
-    return best;
-}
-/* gpu-d1/src/sim.h:254-269 */
-static void act(OState *s, const D1Config *c, const uint16_t *dist, int id) {
-    s->energy[id] = (int16_t)(s->energy[id] - 10);
-    if (cheb(s->pos[id], s->player) == 1) { attack(s, c, id); return; }
-    int q = choose_move(s, c, dist, id);
-    if (q >= 0) {
-        s->occ[s->pos[id]] = -1;
-        s->pos[id] = (int16_t)q;
-        s->occ[q] = (int16_t)id;
     }
 }
 /* LOS-gated waking, gpu-d1/branches/d1-stairs-v2/src/learn.cu:201-207; the v1
@@ -467,11 +487,12 @@ static void primitive(OState *s, const D1Config *c, int d, float *out8, int *saw
             if (s->mhp[i] > 0 && !s->awake[i]) s->energy[i] = -30000;
         for (int i = 0; i < c->count; i++)
             if (s->mhp[i] > 0) s->energy[i] = (int16_t)(s->energy[i] + kind_of(s, c, i)->speed);
+        OMonsters mon = env_monsters(s, c);
         while (s->hp > 0) {
-            int id = scan(s, c->count);
+            int id = o_m_scan(s->energy, c->count);
             if (id < 0) break;
             if (!have_dist && cheb(s->pos[id], s->player) != 1) { player_field(s, dist); have_dist = 1; }
-            act(s, c, dist, id);
+            o_m_act(&mon, dist, id);
             if (in_view(s, s->pos[id]) && s->awake[id]) awake_seen = 1;
         }
     }
@@ -633,12 +654,9 @@ int o_step(OState *st, int n, const D1Config *c, const int64_t *actions, uint8_t
  * of the world after step k. Used only to pin the rule core against sim.h. */
 typedef struct WaitWorld {
     ORng rng;
-    int hp, regen, blocks, fixture, episode;
+    int32_t hp, regen, blocks, fixture, episode;
     int16_t pos[64], energy[64], occ[N];
 } WaitWorld;
-static int wait_better(const WaitWorld *w, int i, int j) {
-    return j < 0 || w->energy[i] > w->energy[j] || (w->energy[i] == w->energy[j] && i < j);
-}
 static void wait_reset(WaitWorld *w, int count, const int32_t *cfg, const int16_t *starts, int first) {
     if (!first) for (int i = 0; i < count; i++) w->occ[w->pos[i]] = -1;
     w->hp = cfg[2]; w->regen = 0; w->blocks = 0;
@@ -648,54 +666,6 @@ static void wait_reset(WaitWorld *w, int count, const int32_t *cfg, const int16_
         w->energy[i] = (int16_t)(70 + rng_r(&w->rng, 10));
     }
     if (!first) w->episode++;
-}
-static void wait_attack(WaitWorld *w, const int32_t *cfg, const int32_t *kinds, int id) {
-    ORng *r = &w->rng;
-    const int32_t *k = kinds + 4 * (id % 6);
-    int hit = rng_r(r, k[2] + 1);
-    int ev = rng_round(r, cfg[4], 100);
-    ev = rng_avg(r, 2 * ev);
-    int margin = hit - ev;
-    if (rng_r(r, 100) < 5) margin = (rng_r(r, 2) ? 1 : -1) * 1000;
-    int bypass = rng_r(r, k[3]);
-    int sh = rng_round(r, cfg[5], 100);
-    int block = rng_avg(r, sh * 2) / 3 - 1;
-    if (block >= bypass && w->blocks < cfg[6]) { w->blocks++; return; }
-    if (margin < 0) return;
-    int damage = 1 + rng_r(r, k[1]);
-    int ac = rng_round(r, cfg[3], 100);
-    int gac = rng_round(r, cfg[3], 100);
-    int gdr = cfg[9 + gac - cfg[3] / 100];
-    int saved = rng_r(r, ac + 1);
-    int half = rng_round(r, ac, 2);
-    saved = imax(saved, imin(gdr * k[1] / 100, half));
-    w->hp -= imax(0, damage - saved);
-}
-static int wait_move(WaitWorld *w, const int32_t *cfg, const uint8_t *floor, const uint16_t *dist, int id) {
-    int player = cfg[1], p = w->pos[id], best = -1, bd = dist[p], ties = 0, rotation = rng_r(&w->rng, 4);
-    for (int z = 0; z < 8; z++) {
-        int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
-        int q = neighbor(p, d);
-        if (q < 0 || !floor[q] || q == player || w->occ[q] >= 0) continue;
-        int dd = dist[q];
-        if (dd < bd) { bd = dd; best = q; ties = 1; }
-        else if (dd == bd && best >= 0 && rng_r(&w->rng, ++ties) == 0) best = q;
-    }
-    if (best >= 0 || !cfg[8]) return best;
-    int cells[24], first[24], len = 1;
-    cells[0] = p; first[0] = -1;
-    for (int head = 0; head < len; head++)
-        for (int d = 0; d < 8; d++) {
-            int q = neighbor(cells[head], d);
-            if (q < 0 || !floor[q] || q == player || w->occ[q] >= 0) continue;
-            int seen = 0;
-            for (int j = 0; j < len; j++) if (cells[j] == q) { seen = 1; break; }
-            if (seen) continue;
-            int step = head == 0 ? q : first[head];
-            if (dist[q] < dist[p]) return step;
-            if (len < 24) { cells[len] = q; first[len] = step; len++; }
-        }
-    return -1;
 }
 static void wait_step(WaitWorld *w, int count, int heap_order, const int32_t *cfg, const int32_t *kinds,
                       const uint8_t *floor, const uint16_t *dist, const int16_t *starts) {
@@ -707,14 +677,12 @@ static void wait_step(WaitWorld *w, int count, int heap_order, const int32_t *cf
     /* The heap and the scan pick the same actor (gpu-d1/src/bench.cu:363-371); the
      * oracle always scans, `heap_order` only selects which reference run it mirrors. */
     (void)heap_order;
+    OMonsters m = {&w->rng, &w->hp, &w->blocks, w->pos, w->energy, w->occ, floor, NULL, kinds,
+                   cfg[1], cfg[3], cfg[4], cfg[5], cfg[6], cfg[8], cfg[9], cfg[10]};
     while (w->hp > 0) {
-        int id = -1;
-        for (int i = 0; i < count; i++) if (w->energy[i] >= 80 && wait_better(w, i, id)) id = i;
+        int id = o_m_scan(w->energy, count);
         if (id < 0) break;
-        w->energy[id] = (int16_t)(w->energy[id] - 10);
-        if (cheb(w->pos[id], cfg[1]) == 1) { wait_attack(w, cfg, kinds, id); continue; }
-        int q = wait_move(w, cfg, floor, dist, id);
-        if (q >= 0) { w->occ[w->pos[id]] = -1; w->pos[id] = (int16_t)q; w->occ[q] = (int16_t)id; }
+        o_m_act(&m, dist, id);
     }
 }
 static uint32_t wait_digest(const WaitWorld *w, int count) {

@@ -57,9 +57,28 @@ typedef struct LState {
     int16_t frontier_cells[O_N], frontier_slot[O_N];
 } LState;
 
+/* The monster rules of gpu-d1/src/sim.h:130-269 (melee, scheduler, greedy move with the
+ * 24-node repair search, act), written once for every world type of this oracle: the env
+ * worlds (OState), the learning-task worlds (LState) and the wait-benchmark worlds all hand
+ * the same functions a view of their fields, so the sim.h golden traces that pin these
+ * functions through the wait worlds pin the code the other two run. */
+typedef struct OMonsters {
+    ORng *rng;
+    int32_t *hp, *blocks;               /* the player's */
+    int16_t *pos, *energy, *occ;        /* occ[5600]: monster id on the cell or -1 */
+    const uint8_t *floor;               /* byte per cell, nonzero = floor */
+    const uint8_t *kind_of;             /* kind index per monster, or NULL for id % 6 */
+    const int32_t *kinds;               /* 6 x {speed, damage, tohit, bypass} */
+    int32_t player, ac100, ev100, sh100, shield_limit, repair, gdr0, gdr1;
+} OMonsters;
+
 #ifdef __cplusplus
 extern "C" {
 #endif
+int o_m_scan(const int16_t *energy, int count);                       /* sim.h:165-174 */
+void o_m_attack(OMonsters *m, int id);                                /* sim.h:130-163 */
+int o_m_choose_move(OMonsters *m, const uint16_t *dist, int id);      /* sim.h:207-253 */
+void o_m_act(OMonsters *m, const uint16_t *dist, int id);             /* sim.h:254-269 */
 uint64_t o_mix(uint64_t x);
 uint32_t o_rng_next(ORng *g);
 int o_rng_r(ORng *g, int bound);

@@ -275,74 +275,12 @@ void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
 }
 
 /* ------------------------------------------------------------------ monsters (gpu-d1/src/sim.h:130-269) */
-static void attack(LState *s, const D1LConfig *c, int id) {
-    ORng *r = &s->rng;
-    const D1LKind *k = &c->kinds[id % 6];
-    int hit = o_rng_r(r, k->tohit + 1);
-    int ev = o_rng_round(r, c->ev100, 100);
-    ev = o_rng_avg(r, 2 * ev);
-    int margin = hit - ev;
-    if (o_rng_r(r, 100) < 5) margin = (o_rng_r(r, 2) ? 1 : -1) * 1000;
-    int bypass = o_rng_r(r, k->bypass);
-    int sh = o_rng_round(r, c->sh100, 100);
-    int block = o_rng_avg(r, sh * 2) / 3 - 1;
-    if (block >= bypass && s->blocks < c->shield_limit) { s->blocks++; return; }
-    if (margin < 0) return;
-    int damage = 1 + o_rng_r(r, k->damage);
-    int ac = o_rng_round(r, c->ac100, 100);
-    int gac = o_rng_round(r, c->ac100, 100);
-    int gdr = c->gdr[gac - c->ac100 / 100];
-    int saved = o_rng_r(r, ac + 1);
-    int half = o_rng_round(r, ac, 2);
-    saved = imax(saved, imin(gdr * k->damage / 100, half));
-    s->hp -= imax(0, damage - saved);
-}
-static int passable(const LState *s, const D1LTables *t, int q) {
-    return q >= 0 && floor_at(t, s->map_id, q) && q != s->player && s->occ[q] < 0;
-}
-static int choose_move(LState *s, const D1LConfig *c, const D1LTables *t, const uint16_t *dist, int id) {
-    int p = s->pos[id], best = -1, bd = dist[p], ties = 0, rotation = o_rng_r(&s->rng, 4);
-    for (int z = 0; z < 8; z++) {
-        int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
-        int q = nb(p, d);
-        if (!passable(s, t, q)) continue;
-        if (dist[q] < bd) { bd = dist[q]; best = q; ties = 1; }
-        else if (dist[q] == bd && best >= 0 && o_rng_r(&s->rng, ++ties) == 0) best = q;
-    }
-    if (best >= 0 || !c->repair) return best;
-    int cells[24], first[24], len = 1;
-    cells[0] = p;
-    first[0] = -1;
-    for (int head = 0; head < len; head++)
-        for (int d = 0; d < 8; d++) {
-            int q = nb(cells[head], d);
-            if (!passable(s, t, q)) continue;
-            int dup = 0;
-            for (int j = 0; j < len && !dup; j++) dup = cells[j] == q;
-            if (dup) continue;
-            int step = head == 0 ? q : first[head];
-            if (dist[q] < dist[p]) return step;
-            if (len < 24) { cells[len] = q; first[len] = step; len++; }
-        }
-    return -1;
-}
-static int scan(const LState *s, int count) {
-    int best = -1;
-    for (int i = 0; i < count; i++)
-        if (s->energy[i] >= 80 &&
-            (best < 0 || s->energy[i] > s->energy[best] || (s->energy[i] == s->energy[best] && i < best)))
-            best = i;
-    return best;
-}
-static void act(LState *s, const D1LConfig *c, const D1LTables *t, const uint16_t *dist, int id) {
-    s->energy[id] = (int16_t)(s->energy[id] - 10);
-    if (cheb(s->pos[id], s->player) == 1) { attack(s, c, id); return; }
-    int q = choose_move(s, c, t, dist, id);
-    if (q >= 0) {
-        s->occ[s->pos[id]] = -1;
-        s->pos[id] = (int16_t)q;
-        s->occ[q] = (int16_t)id;
-    }
+/* The learning-task world's view for the oracle's shared monster rules (o_m_*). */
+static OMonsters learn_monsters(LState *s, const D1LConfig *c, const D1LTables *t) {
+    OMonsters m = {&s->rng, &s->hp, &s->blocks, s->pos, s->energy, s->occ, t->floor + (size_t)s->map_id * N, NULL,
+                   (const int32_t *)c->kinds, s->player, c->ac100, c->ev100, c->sh100, c->shield_limit, c->repair,
+                   c->gdr[0], c->gdr[1]};
+    return m;
 }
 
 /* ------------------------------------------------------------------ observation (learn.cu:480-682) */
@@ -479,10 +417,11 @@ static void primitive(LState *s, const D1LConfig *c, const D1LTables *t, int act
         for (int i = 0; i < c->count; i++)
             if (s->mhp[i] > 0) s->energy[i] = (int16_t)(s->energy[i] + c->kinds[i % 6].speed);
         const uint16_t *dist = field_of(t, s->map_id, s->player);
+        OMonsters mon = learn_monsters(s, c, t);
         while (s->hp > 0) {
-            int id = scan(s, c->count);
+            int id = o_m_scan(s->energy, c->count);
             if (id < 0) break;
-            act(s, c, t, dist, id);
+            o_m_act(&mon, dist, id);
             if (in_view(s, t, s->pos[id])) { out[33] = 1.f; if (s->awake[id]) out[41] = 1.f; }
         }
     }
