@@ -13,6 +13,7 @@
  * compared bit for bit).
  */
 #include "d1_oracle.h"
+#include <stddef.h>
 #include <string.h>
 #include <stdlib.h>
 #ifdef _OPENMP
@@ -558,7 +559,7 @@ void o_obs(const OState *s, const D1Config *c, uint8_t *o) {
             int vis = in_view(s, p);
             ch[2] = (uint8_t)vis;
             int id = s->occ[p];
-            if (vis && id >= 0) { ch[3] = (uint8_t)(s->kind[id] + 1); ch[4] = (uint8_t)imin(s->mhp[id], 255); }
+            if (vis && id >= 0 && s->mhp[id] > 0) { ch[3] = (uint8_t)(s->kind[id] + 1); ch[4] = (uint8_t)imin(s->mhp[id], 255); }
             for (int k = 0; k < 3; k++) if (s->stairs[k] == p && seen_at(s, p)) ch[6] = 1;
             if (seen_at(s, p))
                 for (int d = 0; d < 8; d++) {
@@ -601,6 +602,41 @@ uint32_t o_hash(const OState *s, const D1Config *c) {
 
 /* ------------------------------------------------------------------ batch API */
 int o_state_bytes(void) { return (int)sizeof(OState); }
+
+/* Single-world hooks for the restated reference fixtures (tests/test_env_oracle_fixtures.py).
+ * o_field_offset(k): byte offset of the k-th OState field in declaration order (k = 0..30),
+ * sizeof(OState) for k = 31. */
+int o_field_offset(int k) {
+    static const int off[] = {
+        (int)offsetof(OState, rng), (int)offsetof(OState, env_id), (int)offsetof(OState, t),
+        (int)offsetof(OState, episode), (int)offsetof(OState, player), (int)offsetof(OState, hp),
+        (int)offsetof(OState, regen), (int)offsetof(OState, blocks), (int)offsetof(OState, ticks),
+        (int)offsetof(OState, killed), (int)offsetof(OState, decisions), (int)offsetof(OState, floor_seen),
+        (int)offsetof(OState, first_stair_tick), (int)offsetof(OState, stairs), (int)offsetof(OState, ncells),
+        (int)offsetof(OState, vis_origin), (int)offsetof(OState, vis), (int)offsetof(OState, pos),
+        (int)offsetof(OState, mhp), (int)offsetof(OState, energy), (int)offsetof(OState, awake),
+        (int)offsetof(OState, kind), (int)offsetof(OState, occ), (int)offsetof(OState, viewed),
+        (int)offsetof(OState, floor), (int)offsetof(OState, cells), (int)offsetof(OState, rng.state),
+        (int)offsetof(OState, rng.inc), (int)offsetof(OState, rng.mode), (int)offsetof(OState, rng.k),
+        (int)offsetof(OState, rng.t), (int)sizeof(OState)};
+    return k >= 0 && k < (int)(sizeof off / sizeof off[0]) ? off[k] : -1;
+}
+/* An empty world on a given map: every field zero, the byte floor and spawnable-cell masks
+ * copied, occupancy cleared, no player view memoised, stairs absent. */
+void o_world_map(OState *s, const uint8_t *floor, const uint8_t *cells) {
+    memset(s, 0, sizeof *s);
+    memcpy(s->floor, floor, N);
+    for (int p = 0; p < N; p++) {
+        s->occ[p] = -1;
+        if (cells[p]) s->cells[s->ncells++] = (int16_t)p;
+    }
+    s->vis_origin = -1;
+    s->first_stair_tick = -1;
+    for (int k = 0; k < 3; k++) s->stairs[k] = -1;
+}
+void o_reset(OState *s, const D1Config *c) { reset(s, c); }
+int o_reveal(OState *s) { return reveal(s); }
+void o_transition(OState *s, const D1Config *c, int action, float *out8) { transition(s, c, action, out8); }
 
 static void init_one(OState *s, uint32_t env, const D1Config *c, const uint8_t *floor,
                      const uint8_t *cells, uint64_t seed) {

@@ -98,6 +98,11 @@ int o_step(OState *st, int n, const D1Config *c, const int64_t *actions, uint8_t
 void o_obs(const OState *s, const D1Config *c, uint8_t *obs);
 uint32_t o_hash(const OState *s, const D1Config *c);
 int o_heuristic(OState *s, const D1Config *c);
+int o_field_offset(int k);
+void o_world_map(OState *s, const uint8_t *floor, const uint8_t *cells);
+void o_reset(OState *s, const D1Config *c);
+int o_reveal(OState *s);
+void o_transition(OState *s, const D1Config *c, int action, float *out8);
 /* single-function hooks compared against the reference's sim.h */
 void o_rng_ops(int mode, uint64_t seed, uint64_t seq, int nops, const int32_t *ops,
                const int32_t *args, int32_t *results, uint64_t *final_state);

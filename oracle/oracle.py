@@ -77,20 +77,92 @@ class OracleEnv:
         return np.array([self.L.o_heuristic(self.state[i:].ctypes.data, C.byref(self.cfg)) for i in range(self.batch)],
                         np.int64) if n else None
 
-    # canonical fields (OState layout in oracle/d1_oracle.h)
     def fields(self):
-        dt = np.dtype([('rng_state', '<u8'), ('rng_inc', '<u8'), ('key0', '<u4'), ('key1', '<u4'), ('rt', '<u4'),
-                       ('renv', '<u4'), ('domain', '<u4'), ('k', '<u4'), ('mode', '<i4'), ('pad', '<i4'),
-                       ('env_id', '<u4'), ('t', '<u4'), ('episode', '<i4'), ('player', '<i4'), ('hp', '<i4'),
-                       ('regen', '<i4'), ('blocks', '<i4'), ('ticks', '<i4'), ('killed', '<i4'),
-                       ('decisions', '<i4'), ('floor_seen', '<i4'), ('first_stair_tick', '<i4'),
-                       ('stairs', '<i4', 3), ('ncells', '<i4'), ('vis_origin', '<i4'), ('vis', '<u4', 10), ('pos', '<i2', 64), ('mhp', '<i2', 64),
-                       ('energy', '<i2', 64), ('awake', 'u1', 64), ('kind', 'u1', 64), ('occ', '<i2', 5600),
-                       ('viewed', 'u1', 5600), ('floor', 'u1', 5600), ('cells', '<i2', 5600)])
-        assert dt.itemsize <= self.state.shape[1]
-        return np.frombuffer(self.state.tobytes(), dtype=np.dtype({'names': dt.names, 'formats': [dt.fields[n][0] for n in dt.names],
-                                                                  'offsets': [dt.fields[n][1] for n in dt.names],
-                                                                  'itemsize': self.state.shape[1]}))
+        """Structured copy of the worlds (OState, oracle/d1_oracle.h)."""
+        return self.state.reshape(-1).view(ostate_dtype()).copy()
+
+
+OSTATE_FIELDS = [('rng', 'u1', 48), ('env_id', '<u4'), ('t', '<u4'), ('episode', '<i4'), ('player', '<i4'),
+                 ('hp', '<i4'), ('regen', '<i4'), ('blocks', '<i4'), ('ticks', '<i4'), ('killed', '<i4'),
+                 ('decisions', '<i4'), ('floor_seen', '<i4'), ('first_stair_tick', '<i4'), ('stairs', '<i4', 3),
+                 ('ncells', '<i4'), ('vis_origin', '<i4'), ('vis', '<u4', 10), ('pos', '<i2', 64),
+                 ('mhp', '<i2', 64), ('energy', '<i2', 64), ('awake', 'u1', 64), ('kind', 'u1', 64),
+                 ('occ', '<i2', 5600), ('viewed', 'u1', 5600), ('floor', 'u1', 5600), ('cells', '<i2', 5600),
+                 ('rng_state', '<u8'), ('rng_inc', '<u8'), ('rng_mode', '<i4'), ('rng_k', '<u4'), ('rng_t', '<u4')]
+
+
+def ostate_dtype():
+    """OState as a numpy record, offsets read from the library (o_field_offset)."""
+    L = lib()
+    L.o_field_offset.argtypes = [C.c_int]
+    off = [L.o_field_offset(k) for k in range(len(OSTATE_FIELDS) + 1)]
+    formats = [(f[1], f[2]) if len(f) == 3 else f[1] for f in OSTATE_FIELDS]
+    return np.dtype({'names': [f[0] for f in OSTATE_FIELDS], 'formats': formats, 'offsets': off[:-1],
+                     'itemsize': off[-1]})
+
+
+class OracleWorld:
+    """One env world of the CPU restatement built by hand, for the restated reference
+    fixtures: `f` is a writable record view of its OState."""
+
+    def __init__(self, floor, cells=None):
+        L = self.L = lib()
+        L.o_world_map.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+        L.o_reset.argtypes = [C.c_void_p, C.c_void_p]
+        L.o_reveal.argtypes = [C.c_void_p]
+        L.o_transition.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+        L.o_pcg_seed.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64]
+        dt = ostate_dtype()
+        self.buf = np.zeros(dt.itemsize, np.uint8)
+        self.f = self.buf.view(dt)[0]
+        floor = np.ascontiguousarray(floor, np.uint8)
+        cells = floor if cells is None else np.ascontiguousarray(cells, np.uint8)
+        L.o_world_map(self.ptr, floor.ctypes.data, cells.ctypes.data)
+
+    @property
+    def ptr(self):
+        return self.buf.ctypes.data
+
+    def seed_pcg(self, seed, seq):
+        """The reference's RNG::seed(seed, seq) (gpu-d1/src/sim.h:29-35), on the world's stream."""
+        self.L.o_pcg_seed(self.ptr, seed, seq)
+
+    def reset(self, cfg):
+        self.L.o_reset(self.ptr, C.byref(cfg))
+
+    def reveal(self):
+        return self.L.o_reveal(self.ptr)
+
+    def transition(self, cfg, action):
+        out = np.zeros(8, np.float32)
+        self.L.o_transition(self.ptr, C.byref(cfg), action, out.ctypes.data)
+        return out
+
+    def put(self, i, p, hp, awake, kind=0):
+        """Monster i on cell p (the reference's `put`, semantic_tests.cu:8)."""
+        f = self.f
+        f['pos'][i], f['mhp'][i], f['awake'][i], f['kind'][i] = p, hp, int(awake), kind
+        f['occ'][p] = i
+
+    def obs(self, cfg):
+        o = np.zeros((15, 15, 8), np.uint8)
+        self.L.o_obs(self.ptr, C.byref(cfg), o.ctypes.data)
+        return o
+
+    def copy(self):
+        w = OracleWorld.__new__(OracleWorld)
+        w.L, w.buf = self.L, self.buf.copy()
+        w.f = w.buf.view(self.f.dtype)[0]
+        return w
+
+    def state_bytes(self):
+        """The world's bytes without the view memo (vis_origin, vis), which is not state."""
+        b = self.buf.copy()
+        dt = self.f.dtype
+        for name in ('vis_origin', 'vis'):
+            off = dt.fields[name][1]
+            b[off:off + dt.fields[name][0].itemsize] = 0
+        return b
 
 
 def level(seed, env):
