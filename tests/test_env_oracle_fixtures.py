@@ -259,3 +259,49 @@ def test_descent_leaves_enemies_alive():
     w.reveal()
     out = w.transition(c, DESCEND)
     assert out[2] == 1 and out[3] == 0
+
+
+# ---------------------------------------------------------------- gpu-d1/src/learn.cu:677-707 (learn_semantic_test)
+def v1_world():
+    """learn_semantic_test's world: the v1 rules on the fixture map with one monster,
+    seed(123, 1), and the first floor cell p with a floor neighbour q (direction d)."""
+    c = pkg.config.v1_config(1)
+    floor, cells = pkg.shared_map_arrays()
+    w = O.OracleWorld(floor, cells)
+    w.seed_pcg(123, 1)
+    w.reset(c)
+    for p in np.flatnonzero(cells):
+        for d, (dx, dy) in enumerate(((0, -1), (1, 0), (0, 1), (-1, 0), (1, -1), (1, 1), (-1, 1), (-1, -1))):
+            x, y = int(p) % W + dx, int(p) // W + dy
+            if 0 <= x < W and 0 <= y < 70 and floor[y * W + x]:
+                return w, c, int(p), y * W + x, d
+
+
+def test_v1_free_move_kill_deadline_and_death():
+    w, c, p, q, d = v1_world()
+    # free movement (:684-687)
+    w.f['occ'][:] = -1
+    w.f['player'], w.f['pos'][0], w.f['mhp'][0], w.f['energy'][0], w.f['killed'] = p, q, 0, -30000, 0
+    out = w.transition(c, d)
+    assert w.f['player'] == q and out[1] == 0
+    # killing the last monster ends the episode before it can retaliate, then resets (:688-696):
+    # +1000 kill, +3000 clear, -1 turn; the outcome row keeps the kill count and full HP
+    for k in range(100):
+        w.f['occ'][:] = -1
+        w.f['player'], w.f['pos'][0], w.f['occ'][q], w.f['mhp'][0], w.f['energy'][0] = p, q, 0, 1, 79
+        w.f['hp'], w.f['regen'], w.f['killed'], w.f['ticks'] = c.hp, 0, 0, 0
+        out = w.transition(c, 8 + d)
+        if out[2]:
+            assert out[0] > 3.9 and out[3] == 1 and out[4] == c.hp
+            break
+        assert k < 99
+    # a deadline is terminal with the timeout flag, not the death flag (:697-699)
+    w.reset(c)
+    w.f['ticks'], w.f['energy'][0] = c.limit - 1, -30000
+    out = w.transition(c, WAIT)
+    assert out[1] == 1 and out[7] == 1 and out[6] == 0 and w.f['ticks'] == 0
+    # death terminates and reports the pre-reset HP (clamped at 0) (:700-702)
+    w.reset(c)
+    w.f['hp'], w.f['regen'] = -100, 0
+    out = w.transition(c, WAIT)
+    assert out[6] == 1 and out[4] == 0 and w.f['hp'] == c.hp

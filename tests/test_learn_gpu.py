@@ -127,3 +127,43 @@ def test_error_codes(L, pkg):
     assert lib.learn_turn_cost() == np.float32(1e-5) and lib.learn_return_gamma() == 1.0
     assert (lib.learn_obs_size(), lib.learn_action_size(), lib.learn_out_size(), lib.learn_config_bytes()) == \
         (1015, 19, 45, 140)
+
+
+def test_parity_at_scale_slice(L, O):
+    """8,192 worlds x 256 steps on four maps (map 1057 + three generated levels, first
+    episodes balanced over the maps, clumped placement in a third of resets): worlds are
+    independent and keyed by their index, so the first 512 are replayed by the restatement.
+    Observation (bit patterns), mask and the 45 outcome fields every step, the controller's
+    actions every 4th, the full world state every 16th (the reference's rows:
+    gpu-d1/branches/d1-stairs-v2/src/learn.cu:891-946)."""
+    floors = [O.pkg.data.map1057()['floor']] + gen_floors(O, 3, seed=23)
+    maps = L.LearnMaps(np.stack(floors))
+    host = O.LearnTablesHost(np.stack(floors))
+    n, n_cpu, steps, seed = 8192, 512, 256, 1234
+    env = L.LearnEnv(n, seed=seed, maps=maps, map_filter=-2, clump=1)
+    ref = O.OracleLearn(n_cpu, host, seed=seed, clump=1, map_filter=-2, threads=16)
+    rng = np.random.default_rng(seed)
+    for step in range(steps):
+        if step % 16 == 0:
+            print(f'learn parity at scale: step {step}', flush=True)
+            compare_state_slice(L, O, env, ref, step, n_cpu)
+        h = env.heuristic()
+        if step % 4 == 0:
+            assert np.array_equal(h[:n_cpu].cpu().numpy(), ref.heuristic()), f'heuristic at step {step}'
+        if step % 3 == 2:
+            a = torch.from_numpy(rng.integers(-1, 21, n).astype(np.int64)).cuda()
+        else:
+            a = h
+        env.step(a)
+        assert ref.step(a[:n_cpu].cpu().numpy()) == 0
+        assert np.array_equal(env.obs[:n_cpu].cpu().numpy().view(np.uint32), ref.obs.view(np.uint32)), f'obs {step}'
+        assert np.array_equal(env.mask[:n_cpu].cpu().numpy(), ref.mask), f'mask at step {step}'
+        assert np.array_equal(env.out[:n_cpu].cpu().numpy().view(np.uint32), ref.out.view(np.uint32)), f'out {step}'
+    compare_state_slice(L, O, env, ref, steps, n_cpu)
+    assert ref.scalar('episode').sum() > 0 and ref.scalar('placement_clumped').any()
+
+
+def compare_state_slice(L, O, env, ref, step, n_cpu):
+    class Rows:   # the first n_cpu state rows of the GPU batch, as compare_state reads them
+        state = env.state[:n_cpu]
+    compare_state(L, O, Rows, ref, step)

@@ -302,3 +302,88 @@ def test_frontier_list_is_the_anchor_set(O, pkg):
             anchors = np.flatnonzero((floor & viewed & unviewed_nb).reshape(-1))
             assert sorted(lst) == list(anchors)
             assert np.array_equal(f['frontier_slot'][lst], np.arange(n))
+
+
+# ---------------------------------------------------------------- branches/semantic-actions-v1/src/semantic_tests.cu:3-45
+def semantic_room(O):
+    """The 12x5 test room the reference's preflight compiles around (40, 35)
+    (branches/semantic-actions-v1/scripts/preflight.py:12)."""
+    f = np.zeros(N, np.uint8)
+    for x in range(-2, 10):
+        for y in range(-2, 3):
+            f[(35 + y) * W + 40 + x] = 1
+    return O.LearnTablesHost([f])
+
+
+def isolated(O, maps, cfg, hp=3):
+    """semantic_tests.cu:3-7: all-zero world, player at (40, 35), REQUIRED-1 kills, every
+    enemy dead with -30000 energy, no stairs, the view revealed."""
+    buf, f = blank(O, maps)
+    f['stairs'][:] = -1
+    f['energy'][:] = -30000
+    setv(f, 'player', 35 * W + 40)
+    setv(f, 'hp', hp)
+    setv(f, 'killed', 23)
+    setv(f, 'first_stair_tick', -1)
+    import ctypes as C
+    O.learn_lib().lo_reveal(buf.ctypes.data, C.byref(maps.tables()))
+    return buf, f
+
+
+def put(f, i, p, hp, awake):
+    f['pos'][i], f['mhp'][i], f['awake'][i] = p, hp, int(awake)
+    f['occ'][p] = i
+
+
+def transition(O, buf, maps, cfg, action, limit=2048):
+    import ctypes as C
+    out = np.zeros(45, np.float32)
+    O.learn_lib().lo_transition(buf.ctypes.data, C.byref(cfg), C.byref(maps.tables()), action, limit, out.ctypes.data, 0)
+    return out
+
+
+def test_semantic_rest_sleep_deadline_invalid(O, pkg):
+    """The reference's semantic self-test on its 45-field outcome row: REST equals the WAIT
+    turns it stands for (world bytes, reward, out[26] and out[35] turn counts, out[36]
+    completed, out[37] not interrupted, out[40] the return at learn_return_gamma() = 1);
+    a sleeper at seven tiles lets the REST complete, one at six wakes and interrupts it
+    after one turn; the deadline is exact inside a REST; an ATTACK with no target is one
+    WAIT turn."""
+    maps = semantic_room(O)
+    cfg = pkg.config.learn_config()
+    base, f = isolated(O, maps, cfg)
+    macro, manual = base.copy(), base.copy()
+    out = transition(O, macro, maps, cfg, 17)
+    count, reward = 0, np.float32(0)
+    while True:
+        step = transition(O, manual, maps, cfg, 16)
+        count += 1
+        reward = np.float32(reward + step[0])
+        if getv(manual.view(O.lstate_dtype())[0], 'hp') >= cfg.hp:
+            break
+    setv(manual.view(O.lstate_dtype())[0], 'decisions', 1)
+    assert count > 1 and out[0] == reward and out[40] == reward
+    assert out[26] == count and out[35] == count and out[36] == 1 and out[37] == 0
+    assert np.array_equal(macro, manual)
+
+    sleepy = base.copy()
+    s = sleepy.view(O.lstate_dtype())[0]
+    put(s, 0, 35 * W + 47, 8, False)
+    out = transition(O, sleepy, maps, cfg, 17)
+    assert out[36] == 1 and out[37] == 0 and not s['awake'][0]
+    waking = base.copy()
+    s = waking.view(O.lstate_dtype())[0]
+    put(s, 0, 35 * W + 46, 8, False)
+    out = transition(O, waking, maps, cfg, 17)
+    assert out[26] == 1 and out[37] == 1 and s['awake'][0]
+
+    deadline = base.copy()
+    s = deadline.view(O.lstate_dtype())[0]
+    setv(s, 'ticks', 2047)
+    out = transition(O, deadline, maps, cfg, 17)
+    assert out[1] == 1 and out[7] == 1 and out[5] == 2048 and out[26] == 1 and getv(s, 'ticks') == 0
+
+    invalid = base.copy()
+    s = invalid.view(O.lstate_dtype())[0]
+    out = transition(O, invalid, maps, cfg, 8)
+    assert out[26] == 1 and getv(s, 'ticks') == 1
