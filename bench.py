@@ -1,13 +1,17 @@
 #!/usr/bin/env python3
-"""Benchmark of the D:1 rollout hot path on one MI355X.
+"""Benchmark of the D:1 rollout hot path on one MI355X, with C4, the
+training loop, C5 and the CPU baseline beside it.
 
 One step = one pass over 65,536 worlds: the HIP env step (transition + auto-reset +
-15x15x8 uint8 observation + state hash), the bf16 policy MLP 1800->256->256 with a
-16-logit head and a value head (hipBLASLt via torch), and the counter-RNG categorical
-sampler (HIP) that produces the next actions. Inputs stay resident in HBM; the timed
-region is bracketed by synchronisations. Prints one JSON line.
+15x15x8 uint8 observation) and the fused HIP policy kernel (bf16 MLP 1800->256->256 with a
+16-logit head and a value head on MFMA, then the counter-RNG categorical sample of the next
+actions). Inputs stay resident in HBM; the timed region is bracketed by synchronisations.
+Prints one JSON line: C3 decisions/s as `value`, then `ppo` (C4 samples/s, median of three
+updates after a warm one), `train` (rollout + update iterations), `stress` (C5 at 262,144
+worlds with 40 monsters) and `cpu_baseline` (C1 on the CPU restatement at 1 thread and at
+this job's CPU share).
 
-  python bench.py [--steps K] [--warmup W] [--envs N] [--gpus 1]
+  python bench.py [--steps K] [--warmup W] [--envs N] [--gpus 1] [--mode ...]
 """
 import argparse
 import importlib
@@ -41,14 +45,28 @@ def measured_traffic(path=ROOT / 'profiles' / 'k_step_hbm_traffic.md'):
     return None
 
 
-def cpu_baseline(envs=1024, steps=1000, runs=3, threads=None):
-    """The CPU restatement (oracle/, OpenMP over worlds) on config C1: 1,024 generated
-    levels, 8 monsters, uniform random actions over 16, 1,000 steps; `runs` independent
-    runs (seeds 1, 2, ...) so that the sample is 10-20 s of CPU work."""
+def host_cpus():
+    """(threads this job may use, nproc, CPU model): the affinity mask is what `nproc`
+    reports; a GPU box shares its host with other jobs, one CPU share of 16 per GPU."""
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else (os.cpu_count() or 1)
+    model = 'unknown'
+    try:
+        for line in pathlib.Path('/proc/cpuinfo').read_text().splitlines():
+            if line.startswith('model name'):
+                model = line.split(':', 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return min(16, nproc), nproc, model
+
+
+def cpu_c1(threads, envs=1024, steps=1000, runs=1):
+    """C1 on the CPU restatement (oracle/, OpenMP over worlds, schedule(static) as
+    gpu-d1/src/bench.cu:167-184): `runs` runs of 1,024 generated levels x 1,000 steps,
+    8 monsters, uniform random actions over 16; returns (decisions/s, seconds)."""
     import numpy as np
     from oracle import oracle as O
     pkg = importlib.import_module('dcss-auto_amd')
-    threads = threads or min(16, os.cpu_count() or 1)
     dt = 0.0
     for r in range(runs):
         env = O.OracleEnv(envs, pkg.baseline_config(), seed=1 + r, threads=threads)
@@ -57,9 +75,20 @@ def cpu_baseline(envs=1024, steps=1000, runs=3, threads=None):
         for k in range(steps):
             env.step(actions[k])
         dt += time.perf_counter() - t0
-    return {'value': runs * envs * steps / dt, 'unit': 'env decisions/s', 'cores': threads, 'kind': 'port',
-            'sample': f'C1 full, {runs} runs: {envs} generated levels x {steps} steps each, 8 monsters, '
-                      f'random actions, step+obs+hash, {dt:.2f} s wall on {threads} threads'}
+    return runs * envs * steps / dt, dt
+
+
+def cpu_baseline():
+    """The CPU path timed beside the GPU: C1 at every thread of this job's CPU share (three
+    runs) and at one thread (one run), about 20 s of CPU work in all."""
+    threads, nproc, model = host_cpus()
+    rate, dt = cpu_c1(threads, runs=3)
+    one, dt1 = cpu_c1(1, runs=1)
+    return {'value': rate, 'unit': 'env decisions/s', 'cores': threads, 'kind': 'port',
+            'sample': f'C1 full (1024 generated levels x 1000 steps, 8 monsters, random actions, step+obs+hash): '
+                      f'3 runs on {threads} threads ({dt:.2f} s wall), 1 run on 1 thread ({dt1:.2f} s)',
+            'single_thread': {'value': one, 'cores': 1},
+            'nproc': nproc, 'cpu_model': model}
 
 
 def ppo_bench(args, env, rollout_model, policy_mod, dev):
@@ -93,15 +122,21 @@ def ppo_bench(args, env, rollout_model, policy_mod, dev):
     else:
         trainer = ppo_mod.FastPPO(model, graph=True)     # explicit fwd/bwd, HIP-graph minibatch step
         trainer._capture(buf)                            # capture once per buffer, outside the timing
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    loss = trainer.update(buf, generator=torch.Generator(device=dev).manual_seed(5))
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    gen = torch.Generator(device=dev).manual_seed(5)
+    trainer.update(buf, generator=gen)                  # warm: first replays, allocator, caches
+    times = []
+    for _ in range(args.ppo_updates):                   # the reference warms twice and times 12
+        torch.cuda.synchronize()                        # (gpu-d1/PERFORMANCE.md:7); the median is reported
+        t0 = time.perf_counter()
+        loss = trainer.update(buf, generator=gen)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
     samples = T * n
     flops = samples * trainer.epochs * (TRUNK_FLOPS + 2 * (1800 * 256 + 2 * 256 * 256 + 2 * 256 * 17))
     return {'metric': 'PPO samples/sec (C4: GAE + 4 epochs x 8,192-sample minibatches)', 'value': samples / dt,
             'unit': 'samples/s', 'sample_epochs_per_s': samples * trainer.epochs / dt, 'update_s': dt,
+            'update_s_all': times, 'timing': f'median of {len(times)} updates after one warm update',
             'n_gpus': 1, 'higher_is_better': True, 'dtype': 'bf16 trunk, fp32 master',
             'loss_terms': [float(v) for v in torch.as_tensor(loss).flatten()[:3]], 'graph': trainer.graph,
             'path': 'autograd eager' if args.eager_ppo else 'explicit fwd/bwd, HIP graph',
@@ -194,6 +229,28 @@ def wait_bench(args, worlds=8192, count=8, chunk=64, waits=4096):
                        'waits_per_kernel': chunk, 'waits_per_world': waits}, 'seconds': dt}
 
 
+def event_stride(steps):
+    """Timed steps per sampled set of per-kernel HIP events: every 8th step of a long run
+    (three event records per step cost the measured loop ~4%), every 2nd of a short one so
+    that the kernel averages still rest on ten or more launches."""
+    return EVERY if steps >= 16 * EVERY else 2
+
+
+def roofline(kernel, achieved, launch_ms, step_bytes, traffic, launches):
+    """The bench line's roofline object: algorithmic GB/s (bytes per world-step x worlds /
+    mean launch time from HIP events in the timed region) against HBM peak, and beside it
+    the counter-based rate: HBM bytes per launch read by rocprofv3 FETCH_SIZE + WRITE_SIZE
+    (copy-kernel calibrated, committed under profiles/) over the same live launch time."""
+    r = {'bound': 'hbm', 'kernel': kernel, 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+         'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic, 'bytes_per_env_step': step_bytes,
+         'avg_launch_ms': launch_ms, 'timed_launches': launches}
+    if traffic:
+        counted = traffic / (launch_ms * 1e-3) / 1e9
+        r['counter_gbs'] = counted
+        r['counter_frac'] = counted / HBM_PEAK_GBS
+    return r
+
+
 def stress_bench(args, envs=262144, horizon=256, warmup=4):
     """C5: 262,144 generated-level worlds with 40 monsters (HP U[40,60], half awake at
     spawn), the bf16 trunk with the autoregressive verb(8) x target(25) head and the HIP
@@ -220,22 +277,22 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
     for t in range(warmup):
         one(t)
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(horizon)]
+    every = event_stride(horizon)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(0, horizon, every)]
     t0 = time.perf_counter()
     for k in range(horizon):
-        one(warmup + k, events[k])
+        one(warmup + k, events[k // every] if k % every == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / horizon
+    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
     achieved = STEP_BYTES[40] * envs / (step_ms * 1e-3) / 1e9
+    traffic = measured_traffic(ROOT / 'profiles' / 'k_step_c5_hbm_traffic.md')
     return {'metric': 'env decisions/sec at 262,144 envs, 40 monsters, AR 8x25 head (C5)',
             'value': envs * horizon / wall, 'unit': 'decisions/s', 'n_gpus': 1, 'higher_is_better': True,
             'ms_per_step': wall / horizon * 1e3,
             'config': {'workload': 'C5', 'envs': envs, 'monsters': 40, 'hp': [40, 60], 'awake_pct': 50,
                        'head': 'AR verb 8 x target 25', 'horizon': horizon},
-            'roofline': {'bound': 'hbm', 'kernel': 'd1::k_step', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
-                         'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'bytes_per_env_step': STEP_BYTES[40],
-                         'avg_launch_ms': step_ms}}
+            'roofline': roofline('d1::k_step', achieved, step_ms, STEP_BYTES[40], traffic, len(events))}
 
 
 # Algorithmic bytes of one learning-task decision (k_learn_step): fp32 observation 4060 +
@@ -250,7 +307,7 @@ def learn_cpu_baseline(envs=4096, steps=500, threads=None):
     1057 with the controller's actions."""
     from oracle import oracle as O
     pkg = importlib.import_module('dcss-auto_amd')
-    threads = threads or min(16, os.cpu_count() or 1)
+    threads = threads or host_cpus()[0]
     env = O.OracleLearn(envs, O.LearnTablesHost(pkg.data.map1057()['floor'][None]), seed=1, threads=threads)
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -294,11 +351,8 @@ def learn_bench(args, warmup=8):
               'scaling': 'weak', 'vs_baseline': None, 'dtype': 'int16/u8 state, fp32 obs',
               'data': 'synthetic: map 1057, 24 enemies, clump mode 1',
               'config': {'workload': 'learn', 'envs': n, 'obs': 'fp32 1015', 'clump': 1},
-              'roofline': {'bound': 'hbm', 'kernel': 'd1::learn::k_learn_step', 'achieved': achieved,
-                           'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS,
-                           'traffic': measured_traffic(ROOT / 'profiles' / 'k_learn_step_learn.md'),
-                           'bytes_per_env_step': LEARN_STEP_BYTES, 'avg_launch_ms': step_ms,
-                           'timed_launches': len(ev)},
+              'roofline': roofline('d1::learn::k_learn_step', achieved, step_ms, LEARN_STEP_BYTES,
+                                   measured_traffic(ROOT / 'profiles' / 'k_learn_step_learn.md'), len(ev)),
               'heuristic_ms': heur_ms, 'step_ms': step_ms,
               'errors': int(env.errors().numel())}
     if not args.no_cpu_baseline:
@@ -322,6 +376,8 @@ def main():
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
     ap.add_argument('--eager-ppo', action='store_true', help='run the PPO update without HIP-graph capture')
     ap.add_argument('--no-ppo', action='store_true', help='rollout mode: skip the C4 PPO and training measurements that follow')
+    ap.add_argument('--no-stress', action='store_true', help='rollout mode: skip the C5 stress measurement that follows')
+    ap.add_argument('--ppo-updates', type=int, default=3, help='timed C4 updates (after one warm update); median reported')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
@@ -388,10 +444,11 @@ def main():
     # per-kernel HIP events on every EVERY-th step of the timed region: an event record costs
     # the stream a few microseconds, so events around every launch would slow the
     # throughput being measured (three per step: ~4%)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, EVERY)]
+    every = event_stride(args.steps)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, every)]
     t0 = time.perf_counter()
     for k in range(args.steps):
-        one_step(args.warmup + k, events[k // EVERY] if k % EVERY == 0 else None)
+        one_step(args.warmup + k, events[k // every] if k % every == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
@@ -416,10 +473,7 @@ def main():
         'config': {'workload': 'C3', 'envs': n, 'monsters': args.monsters, 'obs': '15x15x8 uint8',
                    'policy': '1800-256-256 ReLU, 16 logits + value, bf16', 'sampler': 'Philox counter RNG',
                    'rollout_steps': args.steps},
-        'roofline': {'bound': 'hbm', 'kernel': 'd1::k_step', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': measured_traffic(),
-                     'bytes_per_env_step': step_bytes, 'avg_launch_ms': step_ms,
-                     'timed_launches': len(events)},
+        'roofline': roofline('d1::k_step', achieved, step_ms, step_bytes, measured_traffic(), len(events)),
         'trunk': {'bound': 'mfma', 'achieved': trunk_tflops, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                   'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms},
     }
@@ -429,6 +483,11 @@ def main():
                                              'path', 'config', 'mfma')}
         del ppo
         result['train'] = train_bench(args, dev)
+    if not args.no_stress:   # C5 at its own size: decisions/s and k_step's HBM rate against peak
+        del env
+        torch.cuda.empty_cache()
+        stress = stress_bench(args)
+        result['stress'] = {k: stress[k] for k in ('metric', 'value', 'unit', 'ms_per_step', 'config', 'roofline')}
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline()
     print(json.dumps(result), flush=True)
