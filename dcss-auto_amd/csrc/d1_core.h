@@ -15,17 +15,31 @@ namespace d1 {
 constexpr int W = 80, H = 70, N = 5600, RW = 3;   // 3 dwords per 80-bit row
 constexpr int ROWS_WORDS = H * RW;                // 210
 constexpr int BIG = 1 << 20;
+constexpr int FAR = 1 << 20;    // layer of a cell the distance field does not reach
 
+// A kernel that needs a float staging area once the BFS data is dead defines
+// D1_STAGE_FLOATS before including this header; the area overlays the BFS bitmaps.
+#ifndef D1_STAGE_FLOATS
+#define D1_STAGE_FLOATS 1
+#endif
 struct Smem {
     uint32_t floor[ROWS_WORDS];
     uint32_t viewed[ROWS_WORDS];
     uint32_t occ[ROWS_WORDS];
-    uint32_t reach[ROWS_WORDS];
-    uint32_t front[ROWS_WORDS];
     union {
-        uint8_t dist[N];        // BFS layer mod 256, valid where `reach` is set (monster phase)
-        int32_t rowpre[72];     // inclusive per-row prefix counts (episode reset)
+        struct {
+            uint32_t reach[ROWS_WORDS];
+            uint32_t front[ROWS_WORDS];
+            // BFS layer mod 3 of every reached cell as two bit planes: lay0 = layer % 3 == 1,
+            // lay1 = layer % 3 == 2. Cells that BFS-neighbour each other differ by at most one
+            // layer, so their layers mod 3 fix the sign of every comparison the monster rules make
+            int32_t rowpre[72];   // inclusive per-row prefix counts (episode reset)
+            uint32_t lay0[ROWS_WORDS];
+            uint32_t lay1[ROWS_WORDS];
+        };
+        float stage[D1_STAGE_FLOATS];
     };
+    uint32_t rq[32];   // the repair search's queue (packed entries)
 };
 
 // ---------------------------------------------------------------- small helpers
@@ -36,13 +50,33 @@ __device__ __forceinline__ int iabs(int a) { return a < 0 ? -a : a; }
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ int lane_val(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 __device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
+// DPP lane moves (GFX9 data-parallel primitives, no LDS round trip). `id` fills the lanes
+// whose source is outside the wave or outside the written rows.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp(int v, int id) { return __builtin_amdgcn_update_dpp(id, v, CTRL, ROWS, 0xF, false); }
+constexpr int DPP_QUAD_1032 = 0xB1, DPP_QUAD_2301 = 0x4E, DPP_ROW_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140,
+              DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143, DPP_WAVE_SHL1 = 0x130, DPP_WAVE_SHR1 = 0x138;
+// Whole-wave reductions (every lane active): pairs, quads, half rows and rows by lane
+// permutations, then row 0 into row 1 and row 2 into row 3 (row_bcast:15), rows 0-1 into
+// rows 2-3 (row_bcast:31); lane 63 ends with the wave's result.
+template <typename Op>
+__device__ __forceinline__ int wave_reduce(int v, int id, Op op) {
+    v = op(v, dpp<DPP_QUAD_1032>(v, id));
+    v = op(v, dpp<DPP_QUAD_2301>(v, id));
+    v = op(v, dpp<DPP_ROW_HALF_MIRROR>(v, id));
+    v = op(v, dpp<DPP_ROW_MIRROR>(v, id));
+    v = op(v, dpp<DPP_ROW_BCAST15, 0xA>(v, id));
+    v = op(v, dpp<DPP_ROW_BCAST31, 0xC>(v, id));
+    return __builtin_amdgcn_readlane(v, 63);
+}
 __device__ __forceinline__ int wave_max(int v) {
-    for (int o = 32; o; o >>= 1) v = imax(v, __shfl_xor(v, o));
-    return uni(v);
+    return wave_reduce(v, (int)0x80000000, [](int a, int b) { return imax(a, b); });
+}
+__device__ __forceinline__ int wave_min(int v) {
+    return wave_reduce(v, 0x7FFFFFFF, [](int a, int b) { return imin(a, b); });
 }
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-    for (int o = 32; o; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
-    return (uint32_t)uni((int)v);
+    return (uint32_t)wave_reduce((int)v, 0, [](int a, int b) { return (int)((uint32_t)a + (uint32_t)b); });
 }
 // gpu-d1/src/sim.h:14
 __device__ __forceinline__ int cheb(int a, int b) { return imax(iabs(a % W - b % W), iabs(a / W - b / W)); }
@@ -278,6 +312,8 @@ struct Ctx {
     uint64_t vis0, vis1, vis2, vis3;   // player view, quadrants (+,+) (-,+) (-,-) (+,-)
     // this lane's monster (lane < count)
     int mpos, mhp, menergy, mawake, mkind;
+    int mlay;    // absolute BFS layer of the monster's cell (FAR when not known)
+    int lastl;   // last layer the field holds: a reached cell next to an unreached one is on it
     int lane;
 };
 
@@ -480,115 +516,172 @@ __device__ __forceinline__ void attack(Ctx &x, int kind) {
     damage = imax(0, damage - saved);
     x.hp -= damage;
 }
-// distance of q relative to p (both via the BFS field); BIG when q was not reached
-__device__ __forceinline__ int rel_dist(const Ctx &x, int q, int p) {
-    if (!bit(x.sm->reach, q)) return BIG;
-    return (int)(int8_t)(uint8_t)(x.sm->dist[q] - x.sm->dist[p]);
+// BFS layer mod 3 of cell q (meaningful where reach is set)
+__device__ __forceinline__ int lay3(const Smem *sm, int q) { return (int)bit(sm->lay0, q) | ((int)bit(sm->lay1, q) << 1); }
+// layer(q) - layer(r) from the layers mod 3 of two reached cells whose layers differ by at
+// most one (8-neighbours on the BFS graph): -1, 0 or +1
+__device__ __forceinline__ int step3(int mq, int mr) {
+    const int d = mq - mr;
+    return d == 1 || d == -2 ? 1 : (d == -1 || d == 2 ? -1 : 0);
 }
 __device__ __forceinline__ bool walkable(const Ctx &x, int q) {
     return q >= 0 && bit(x.sm->floor, q) && q != x.player && !bit(x.sm->occ, q);
 }
+// ---------------------------------------------------------------- monster moves in coordinates
+// Direction d (N,E,S,W,NE,SE,SW,NW) as offsets: two bits of dx+1 / dy+1 per direction.
+constexpr uint32_t DXP = 1u | 2u << 2 | 1u << 4 | 0u << 6 | 2u << 8 | 2u << 10 | 0u << 12 | 0u << 14;
+constexpr uint32_t DYP = 0u | 1u << 2 | 2u << 4 | 1u << 6 | 0u << 8 | 2u << 10 | 2u << 12 | 0u << 14;
+__device__ __forceinline__ int ddx(int d) { return (int)((DXP >> (2 * d)) & 3u) - 1; }
+__device__ __forceinline__ int ddy(int d) { return (int)((DYP >> (2 * d)) & 3u) - 1; }
+// The bitmap words of one cell (x, y): walkable (floor, unoccupied, not the player), reached
+// by the distance field, its layer mod 3, queued by the repair search.
+struct Cell {
+    bool walk, reached, queued;
+    int m3;
+};
+__device__ __forceinline__ Cell cell_at(const Smem *sm, int x, int y, int plx, int ply) {
+    Cell c{false, false, false, 0};
+    if ((unsigned)x >= (unsigned)W || (unsigned)y >= (unsigned)H) return c;
+    const int w = y * RW + (x >> 5);
+    const uint32_t b = 1u << (x & 31);
+    c.walk = (sm->floor[w] & b) && !(sm->occ[w] & b) && !(x == plx && y == ply);
+    c.reached = (sm->reach[w] & b) != 0;
+    c.queued = (sm->front[w] & b) != 0;
+    c.m3 = (int)((sm->lay0[w] & b) != 0) | ((int)((sm->lay1[w] & b) != 0) << 1);
+    return c;
+}
+
+// The 24-node detour of gpu-d1/src/sim.h:227-252: a FIFO search from p over walkable cells
+// in direction order N,E,S,W,NE,SE,SW,NW, queueing at most 24 cells; the first neighbour (in
+// head, direction order) of a queued cell that is walkable and lower than p returns the
+// first step towards it. Queue entries live in sm->rq, one packed word each (x, y, the
+// first step's direction from p, layer mod 3, absolute layer or RQ_FAR); sm->front marks
+// queued cells.
+//
+// Up to eight heads are expanded per pass (lane = 8 x head offset + direction), which is the
+// sequential order: heads appended during a pass come after every head of the pass, a lower
+// cell is never queued (it would have returned), and a candidate that also neighbours an
+// earlier head of the pass is that head's to append (it enumerates all eight neighbours and
+// sees the same queued set), so the first occurrences in lane order are appended, in order,
+// while the queue has room. Layers are exact along the queue: a reached neighbour of a
+// reached cell is one of -1/0/+1 away, which the layers mod 3 decide; a reached neighbour of
+// an unreached cell is on the field's last layer; an unreached cell lies beyond every layer
+// that could be lower than p.
+constexpr int REPAIR_Q = 24, RQ_FAR = 8191;
+__device__ __forceinline__ uint32_t rq_pack(int x, int y, int fdir, int m3, int lay) {
+    return (uint32_t)x | (uint32_t)y << 7 | (uint32_t)fdir << 14 | (uint32_t)m3 << 17 | (uint32_t)imin(lay, RQ_FAR) << 19;
+}
+__device__ __forceinline__ int next_layer(const Cell &c, int hlay, int hm, int lastl) {
+    if (!c.reached) return RQ_FAR;
+    return hlay < RQ_FAR ? hlay + step3(c.m3, hm) : lastl;
+}
+// Returns the first step's direction from p (-1: none).
+__device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, int ply, int mp, int plag) {
+    Smem *sm = x.sm;
+    const int hoff = x.lane >> 3, dir = x.lane & 7, dx = ddx(dir), dy = ddy(dir);
+    const int lastl = imin(x.lastl, RQ_FAR - 1);
+    if (x.lane == 0) {
+        sm->rq[0] = rq_pack(px, py, 0, mp, plag);
+        sm->front[py * RW + (px >> 5)] |= 1u << (px & 31);
+    }
+    __syncthreads();
+    int len = 1, head = 0, result = -1;
+    while (head < len && len < REPAIR_Q) {
+        const int nh = imin(8, len - head), h = head + hoff;
+        const uint32_t hw = sm->rq[imin(h, REPAIR_Q - 1)];
+        const int hx = (int)(hw & 127u), hy = (int)((hw >> 7) & 127u), hf = (int)((hw >> 14) & 7u);
+        const int hm = (int)((hw >> 17) & 3u), hlay = (int)(hw >> 19);
+        const bool hv = hoff < nh;
+        const int nx = hx + dx, ny = hy + dy;
+        const Cell c = hv ? cell_at(sm, nx, ny, plx, ply) : Cell{false, false, false, 0};
+        const int nlay = c.walk ? next_layer(c, hlay, hm, lastl) : RQ_FAR;
+        const int fdir = h == 0 ? dir : hf;
+        const uint64_t lm = ballot(c.walk && nlay < plag);
+        if (lm) {
+            result = lane_val(fdir, __ffsll((unsigned long long)lm) - 1);
+            break;
+        }
+        bool cand = c.walk && !c.queued;
+        for (int j = 0; j + 1 < nh; j++) {   // earlier heads of the pass own their neighbours
+            const uint32_t jw = (uint32_t)lane_val((int)hw, 8 * j);
+            const int ex = nx - (int)(jw & 127u), ey = ny - (int)((jw >> 7) & 127u);
+            cand = cand && !(hoff > j && ex >= -1 && ex <= 1 && ey >= -1 && ey <= 1);
+        }
+        const uint64_t cm = ballot(cand);
+        const int cnt = imin(__popcll(cm), REPAIR_Q - len);
+        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(cm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cm, 0u));
+        if (cand && rank < cnt) {
+            sm->rq[len + rank] = rq_pack(nx, ny, fdir, c.m3, nlay);
+            atomicOr(&sm->front[ny * RW + (nx >> 5)], 1u << (nx & 31));
+        }
+        len += cnt;
+        head += nh;
+        __syncthreads();
+    }
+    // Queue full: nothing more is appended and a queued cell is never lower, so the
+    // remaining heads only look for the first lower neighbour, eight heads per pass.
+    for (; result < 0 && head < len; head += 8) {
+        const int h = head + hoff;
+        const uint32_t hw = sm->rq[imin(h, REPAIR_Q - 1)];
+        const int hx = (int)(hw & 127u), hy = (int)((hw >> 7) & 127u), hf = (int)((hw >> 14) & 7u);
+        const int hm = (int)((hw >> 17) & 3u), hlay = (int)(hw >> 19);
+        const Cell c = h < len ? cell_at(sm, hx + dx, hy + dy, plx, ply) : Cell{false, false, false, 0};
+        const int nlay = c.walk ? next_layer(c, hlay, hm, lastl) : RQ_FAR;
+        const uint64_t lm = ballot(c.walk && nlay < plag);
+        if (lm) result = lane_val(h == 0 ? dir : hf, __ffsll((unsigned long long)lm) - 1);
+    }
+    if (x.lane < len) {
+        const uint32_t qw = sm->rq[x.lane];
+        const int qx = (int)(qw & 127u), qy = (int)((qw >> 7) & 127u);
+        atomicAnd(&sm->front[qy * RW + (qx >> 5)], ~(1u << (qx & 31)));
+    }
+    __syncthreads();
+    return result;
+}
 // gpu-d1/src/sim.h:207-253: greedy descent with rotated order and 1/ties
-// replacement, then a bounded 24-node BFS detour when stuck.
-__device__ __forceinline__ int choose_move(Ctx &x, int p) {
+// replacement, then a bounded 24-node BFS detour when stuck. p is a reached cell at
+// absolute layer plag (every mover is reached before the field stops growing); the chosen
+// cell's layer goes to qlag.
+__device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
     int rotation = x.g.r(4);
-    int z = x.lane & 7;
-    int d = z < 4 ? (z + rotation) % 4 : 4 + (z + rotation) % 4;
-    int q = nbr(p, d);
-    bool ok = x.lane < 8 && walkable(x, q);
-    // Reached neighbours differ from p by at most one layer, so only the lower ones
-    // (rel -1) can be chosen: the first in rotated order is taken, each later one
-    // replaces it when r(++ties) == 0. Equal and higher ones neither win nor draw.
-    uint64_t low = ballot(ok && rel_dist(x, q, p) < 0);
+    const Smem *sm = x.sm;
+    const int px = p % W, py = p / W, plx = x.player % W, ply = x.player / W;
+    const Cell pc = cell_at(sm, px, py, plx, ply);
+    const int mp = pc.m3;
+    const int z = x.lane & 7;
+    const int d = z < 4 ? (z + rotation) & 3 : 4 + ((z + rotation) & 3);
+    const int nx = px + ddx(d), ny = py + ddy(d);
+    const Cell c = x.lane < 8 ? cell_at(sm, nx, ny, plx, ply) : Cell{false, false, false, 0};
+    const int q = ny * W + nx;
+    // Reached neighbours differ from p by at most one layer, so only the lower ones can be
+    // chosen: the first in rotated order is taken, each later one replaces it when
+    // r(++ties) == 0. Equal, higher and unreached ones neither win nor draw.
+    uint64_t low = ballot(c.walk && c.reached && step3(c.m3, mp) < 0);
     if (low) {
         int best = lane_val(q, __ffsll((unsigned long long)low) - 1), ties = 1;
         for (low &= low - 1; low; low &= low - 1) {
             int qq = lane_val(q, __ffsll((unsigned long long)low) - 1);
             if (x.g.r(++ties) == 0) best = qq;
         }
+        qlag = plag - 1;
         return best;
     }
     if (!x.c->repair) return -1;
-    // Bounded 24-node BFS detour. Lanes 0..23 hold the queue (cell, first step);
-    // each head expands its 8 directions at once: sm->front marks queued cells, the
-    // first lower candidate in direction order returns, otherwise the new candidates
-    // are appended in direction order while the queue has room.
-    Smem *sm = x.sm;
-    int qcell = x.lane == 0 ? p : -1, qfirst = -1, len = 1, result = -1;
-    if (x.lane == 0) atomicOr(&sm->front[(p / W) * RW + ((p % W) >> 5)], 1u << ((p % W) & 31));
-    __syncthreads();
-    int head = 0;
-    for (; head < len && len < 24; head++) {
-        int cell = lane_val(qcell, head), hfirst = lane_val(qfirst, head);
-        int nq = nbr(cell, x.lane & 7);
-        bool v = x.lane < 8 && walkable(x, nq) && !bit(sm->front, nq);
-        uint64_t vm = ballot(v);
-        if (!vm) continue;
-        int step = head == 0 ? nq : hfirst;
-        uint64_t lm = ballot(v && rel_dist(x, nq, p) < 0);
-        if (lm) {
-            result = lane_val(step, __ffsll((unsigned long long)lm) - 1);
-            break;
-        }
-        int cnt = imin(__popcll(vm), 24 - len);
-        if (cnt <= 0) continue;
-        int k = x.lane - len;
-        bool take = k >= 0 && k < cnt;
-        int src = take ? select64(vm, k) : 0;
-        int cq = __shfl(nq, src), cf = __shfl(step, src);
-        if (take) { qcell = cq; qfirst = cf; }
-        if (v && __popcll(vm & ((1ULL << x.lane) - 1ULL)) < cnt)
-            atomicOr(&sm->front[(nq / W) * RW + ((nq % W) >> 5)], 1u << ((nq % W) & 31));
-        len += cnt;
-        __syncthreads();
-    }
-    // Queue full: nothing more is appended, and a queued cell is never lower, so the
-    // remaining heads only look for the first lower neighbour in (head, direction)
-    // order, eight heads per pass (lane = 8 * head offset + direction).
-    for (; result < 0 && head < len; head += 8) {
-        int h = head + (x.lane >> 3);
-        int cell = __shfl(qcell, imin(h, 23)), hfirst = __shfl(qfirst, imin(h, 23));
-        int nq = nbr(cell, x.lane & 7);
-        uint64_t lm = ballot(h < len && walkable(x, nq) && rel_dist(x, nq, p) < 0);
-        if (lm) result = lane_val(hfirst, __ffsll((unsigned long long)lm) - 1);
-    }
-    if (x.lane < len)
-        atomicAnd(&sm->front[(qcell / W) * RW + ((qcell % W) >> 5)], ~(1u << ((qcell % W) & 31)));
-    __syncthreads();
-    return result;
-}
-// One BFS layer for row y: dilate the frontier rows y-1..y+1 by one cell, keep floor
-// cells not reached yet.
-__device__ __forceinline__ Row bfs_expand(const Smem *sm, int y) {
-    Row v = row_ld(sm->front, y);
-    if (y > 0) v = row_or(v, row_ld(sm->front, y - 1));
-    if (y < H - 1) v = row_or(v, row_ld(sm->front, y + 1));
-    v = row_or(v, row_or(row_shl1(v), row_shr1(v)));
-    return row_andn(row_and(v, row_ld(sm->floor, y)), row_ld(sm->reach, y));
-}
-__device__ __forceinline__ void scatter_layer(Smem *sm, int base, uint32_t b, int layer) {
-    while (b) {
-        int xx = __ffs(b) - 1;
-        b &= b - 1;
-        sm->dist[base + xx] = (uint8_t)layer;
-    }
-}
-__device__ __forceinline__ void bfs_commit(Smem *sm, int y, Row nw, int layer) {
-    row_st(sm->front, y, nw);
-    row_st(sm->reach, y, row_or(row_ld(sm->reach, y), nw));
-    scatter_layer(sm, y * W, nw.a, layer);
-    scatter_layer(sm, y * W + 32, nw.b, layer);
-    scatter_layer(sm, y * W + 64, nw.c, layer);
+    const int fd = repair_search(x, px, py, plx, ply, mp, imin(plag, RQ_FAR - 1));
+    if (fd < 0) return -1;
+    const int sx = px + ddx(fd), sy = py + ddy(fd);
+    const Cell sc = cell_at(sm, sx, sy, plx, ply);   // a reached neighbour of p
+    qlag = plag + step3(sc.m3, mp);
+    return sy * W + sx;
 }
 // Bit-parallel BFS over floor from the player (the all-pairs row of
-// gpu-d1/scripts/learn_env.py:31-39), stopped `margin` layers after every mover is
-// reached. dist holds the layer mod 256; comparisons are relative (|delta| <= 25).
-// Lane l keeps rows l and (l < 6) 64+l of the frontier, reach and floor in registers;
-// vertical neighbours arrive by lane shuffles, so a layer needs no LDS round trip or
-// barrier. Reach is published to LDS at the end (the monster phase reads it), and the
-// frontier bitmap is cleared there for the repair search's queued-cell marks.
-__device__ __forceinline__ uint32_t lane_up(uint32_t v) { return (uint32_t)__shfl_up((int)v, 1); }
-__device__ __forceinline__ uint32_t lane_dn(uint32_t v) { return (uint32_t)__shfl_down((int)v, 1); }
+// gpu-d1/scripts/learn_env.py:31-39), stopped `margin` layers after every mover is reached.
+// Lane l keeps rows l and (l < 6) 64+l of the frontier, reach, floor and the two layer-mod-3
+// planes in registers; vertical neighbours arrive by DPP lane shifts, so a layer has no LDS
+// access and no barrier. Reach and the planes are published to LDS at the end (the monster
+// phase reads them); the frontier bitmap is left clear for the repair search's marks.
+__device__ __forceinline__ uint32_t lane_up(uint32_t v) { return (uint32_t)dpp<DPP_WAVE_SHR1>((int)v, 0); }   // lane l <- l-1
+__device__ __forceinline__ uint32_t lane_dn(uint32_t v) { return (uint32_t)dpp<DPP_WAVE_SHL1>((int)v, 0); }   // lane l <- l+1
 __device__ __forceinline__ Row row_up(Row r) { return {lane_up(r.a), lane_up(r.b), lane_up(r.c)}; }
 __device__ __forceinline__ Row row_dn(Row r) { return {lane_dn(r.a), lane_dn(r.b), lane_dn(r.c)}; }
 __device__ __forceinline__ Row row_lane(Row r, int l) {
@@ -604,59 +697,75 @@ __device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
     const int lane = x.lane;
     const bool has1 = lane < H - 64;
     const Row zero{0, 0, 0};
+    // the movers' cells as bit rows, staged through the (cleared) frontier bitmap
+    row_st(sm->front, lane, zero);
+    if (has1) row_st(sm->front, 64 + lane, zero);
+    __syncthreads();
+    if ((movers >> lane) & 1) atomicOr(&sm->front[(x.mpos / W) * RW + ((x.mpos % W) >> 5)], 1u << ((x.mpos % W) & 31));
+    __syncthreads();
+    const Row mv0 = row_ld(sm->front, lane), mv1 = has1 ? row_ld(sm->front, 64 + lane) : zero;
+    __syncthreads();
+    row_st(sm->front, lane, zero);
+    if (has1) row_st(sm->front, 64 + lane, zero);
     const Row fl0 = row_ld(sm->floor, lane), fl1 = has1 ? row_ld(sm->floor, 64 + lane) : zero;
     const int py = x.player / W, px = x.player % W;
     const Row pbit = row_range(px, px);
     Row f0 = lane == py ? pbit : zero, f1 = has1 && 64 + lane == py ? pbit : zero;
     Row r0 = f0, r1 = f1;
-    if (lane == 0) sm->dist[x.player] = 0;
-    // this lane's monster cell: source lane and word of its row
+    Row a0 = zero, a1 = zero, b0 = zero, b1 = zero;   // layer % 3 == 1, layer % 3 == 2
+    // a mover lane learns its cell's layer when a layer first covers it: its row is held by
+    // lane (row & 63), whose newly reached mover bits are read out once per such lane
     const bool mover = (movers >> lane) & 1;
-    const int my = mover ? x.mpos / W : 0, mx = mover ? x.mpos % W : 0;
-    const int msrc = my & 63, mword = mx >> 5;
-    const uint32_t mbit = 1u << (mx & 31);
-    int stop = 1 << 30;
+    const int my = mover ? x.mpos / W : 0, mword = mover ? (x.mpos % W) >> 5 : 0;
+    const uint32_t mbit = mover ? 1u << ((x.mpos % W) & 31) : 0u;
+    x.mlay = FAR;
+    int m3 = 0, stop = 1 << 30, last = 0;
     for (int layer = 1; layer < N; layer++) {
+        m3 = m3 == 2 ? 0 : m3 + 1;
         const Row f1_0 = row_lane(f1, 0), f0_63 = row_lane(f0, 63);
         const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, f1_0, row_dn(f0));
         const Row u1 = row_sel(lane == 0, f0_63, row_up(f1)), d1 = row_sel(lane >= H - 65, zero, row_dn(f1));
         const Row n0 = row_andn(row_and(dilate(f0, u0, d0), fl0), r0);
         const Row n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), fl1), r1) : zero;
+        if (!ballot(row_any(n0) || row_any(n1))) break;
+        last = layer;
         r0 = row_or(r0, n0); r1 = row_or(r1, n1);
         f0 = n0; f1 = n1;
-        scatter_layer(sm, lane * W, n0.a, layer);
-        scatter_layer(sm, lane * W + 32, n0.b, layer);
-        scatter_layer(sm, lane * W + 64, n0.c, layer);
-        if (has1) {
-            scatter_layer(sm, (64 + lane) * W, n1.a, layer);
-            scatter_layer(sm, (64 + lane) * W + 32, n1.b, layer);
-            scatter_layer(sm, (64 + lane) * W + 64, n1.c, layer);
+        if (m3 == 1) { a0 = row_or(a0, n0); a1 = row_or(a1, n1); }
+        if (m3 == 2) { b0 = row_or(b0, n0); b1 = row_or(b1, n1); }
+        const Row h0 = row_and(n0, mv0), h1 = row_and(n1, mv1);
+        for (uint64_t hit = ballot(row_any(h0) || row_any(h1)); hit; hit &= hit - 1) {
+            const int l = __ffsll((unsigned long long)hit) - 1;
+            const Row g = my >= 64 ? row_lane(h1, l) : row_lane(h0, l);
+            const uint32_t w = mword == 0 ? g.a : mword == 1 ? g.b : g.c;
+            if (mover && (my & 63) == l && (w & mbit)) x.mlay = layer;
         }
-        if (!ballot(row_any(n0) || row_any(n1))) break;
-        if (stop == (1 << 30)) {
-            const Row s0 = {(uint32_t)__shfl((int)r0.a, msrc), (uint32_t)__shfl((int)r0.b, msrc), (uint32_t)__shfl((int)r0.c, msrc)};
-            const Row s1 = {(uint32_t)__shfl((int)r1.a, msrc), (uint32_t)__shfl((int)r1.b, msrc), (uint32_t)__shfl((int)r1.c, msrc)};
-            const Row sr = my >= 64 ? s1 : s0;
-            const uint32_t w = mword == 0 ? sr.a : mword == 1 ? sr.b : sr.c;
-            if (!ballot(mover && !(w & mbit))) stop = layer + margin;
-        }
+        if (stop == (1 << 30) && !ballot(row_any(row_andn(mv0, r0)) || row_any(row_andn(mv1, r1)))) stop = layer + margin;
         if (layer >= stop) break;
     }
+    x.lastl = last;
     row_st(sm->reach, lane, r0);
-    row_st(sm->front, lane, zero);
-    if (has1) { row_st(sm->reach, 64 + lane, r1); row_st(sm->front, 64 + lane, zero); }
+    row_st(sm->lay0, lane, a0);
+    row_st(sm->lay1, lane, b0);
+    if (has1) { row_st(sm->reach, 64 + lane, r1); row_st(sm->lay0, 64 + lane, a1); row_st(sm->lay1, 64 + lane, b1); }
     __syncthreads();
 }
 // gpu-d1/src/sim.h:254-269
+// The mover's absolute layer follows it (the cell it steps to is a reached neighbour).
 __device__ __forceinline__ void act(Ctx &x, int id) {
     if (x.lane == id) x.menergy -= 10;
     int p = lane_val(x.mpos, id);
     if (cheb(p, x.player) == 1) { attack(x, lane_val(x.mkind, id)); return; }
-    int q = choose_move(x, p);
+    int qlag = FAR;
+    int q = choose_move(x, p, lane_val(x.mlay, id), qlag);
     if (q >= 0) {
-        occ_set(x, p, false);
-        occ_set(x, q, true);
-        if (x.lane == id) x.mpos = q;
+        if (x.lane == 0) {   // occupancy follows the monster (one lane, then a wave-wide wait)
+            uint32_t *occ = x.sm->occ;
+            occ[(p / W) * RW + ((p % W) >> 5)] &= ~(1u << ((p % W) & 31));
+            occ[(q / W) * RW + ((q % W) >> 5)] |= 1u << ((q % W) & 31);
+        }
+        __syncthreads();
+        if (x.lane == id) { x.mpos = q; x.mlay = qlag; }
     }
 }
 

@@ -577,20 +577,29 @@ __device__ __forceinline__ void wait_stage_map(Ctx &x, const D1WaitMap &map) {
         int y = x.lane + 64 * s;
         if (y >= H) break;
         for (int j = 0; j < 3; j++) {
-            uint32_t f = 0, r = 0;
+            uint32_t f = 0, r = 0, l0 = 0, l1 = 0;
             for (int b = 0; b < 32 && 32 * j + b < W; b++) {
                 int p = y * W + 32 * j + b;
+                const int d = map.dist[p];
                 f |= (uint32_t)(map.floor[p] != 0) << b;
-                r |= (uint32_t)(map.dist[p] != 65535) << b;
+                r |= (uint32_t)(d != 65535) << b;
+                l0 |= (uint32_t)(d != 65535 && d % 3 == 1) << b;
+                l1 |= (uint32_t)(d != 65535 && d % 3 == 2) << b;
             }
             sm->floor[y * RW + j] = f;
             sm->reach[y * RW + j] = r;
+            sm->lay0[y * RW + j] = l0;
+            sm->lay1[y * RW + j] = l1;
             sm->occ[y * RW + j] = 0;
             sm->front[y * RW + j] = 0;
         }
     }
-    for (int p = x.lane; p < N; p += 64) sm->dist[p] = (uint8_t)map.dist[p];
     __syncthreads();
+}
+// the static field's layer of cell p (FAR where it is unreached)
+__device__ __forceinline__ int wait_layer(const D1WaitMap &map, int p) {
+    const int d = p >= 0 && p < N ? map.dist[p] : 65535;
+    return d == 65535 ? FAR : d;
 }
 // gpu-d1/src/sim.h:93-111
 __device__ __forceinline__ void wait_reset(Ctx &x, const D1WaitMap &map, int count, int fixture, bool first) {
@@ -602,7 +611,7 @@ __device__ __forceinline__ void wait_reset(Ctx &x, const D1WaitMap &map, int cou
         int en = 70 + x.g.r(10);
         if (x.lane == i) { x.mpos = p; x.menergy = en; }
     }
-    if (x.lane < count) occ_set_lane(x, x.mpos);
+    if (x.lane < count) { occ_set_lane(x, x.mpos); x.mlay = wait_layer(map, x.mpos); }
     __syncthreads();
     if (!first) x.episode++;
 }
@@ -627,7 +636,7 @@ __device__ __forceinline__ uint32_t wait_digest(Ctx &x, int count) {
     return h + term((uint32_t)x.hp, 0) + term((uint32_t)x.regen, 1) + term((uint32_t)x.blocks, 2) +
            term((uint32_t)x.episode, 3) + term((uint32_t)x.g.pcg_state(), 4) + term((uint32_t)(x.g.pcg_state() >> 32), 5);
 }
-__device__ __forceinline__ void wait_load(Ctx &x, const uint8_t *row, int count, int &fixture) {
+__device__ __forceinline__ void wait_load(Ctx &x, const D1WaitMap &map, const uint8_t *row, int count, int &fixture) {
     WaitHdr h = *(const WaitHdr *)row;
     x.g.pcg_load(h.rng_state, h.rng_inc);
     x.hp = h.hp; x.regen = h.regen; x.blocks = h.blocks; x.episode = h.episode; fixture = h.fixture;
@@ -637,6 +646,7 @@ __device__ __forceinline__ void wait_load(Ctx &x, const uint8_t *row, int count,
         x.mpos = m[0]; x.menergy = m[1];
         occ_set_lane(x, x.mpos);
     }
+    x.mlay = x.lane < count ? wait_layer(map, x.mpos) : FAR;
     __syncthreads();
 }
 __device__ __forceinline__ void wait_store(Ctx &x, uint8_t *row, int count, int fixture) {
@@ -654,6 +664,8 @@ __device__ __forceinline__ void wait_store(Ctx &x, uint8_t *row, int count, int 
 __device__ __forceinline__ void wait_ctx(Ctx &x, Smem *sm, const D1Config *cfg, const D1WaitMap &map) {
     x.sm = sm; x.c = cfg; x.rays = nullptr; x.nslots = 0; x.lane = lane_id();
     x.player = map.player; x.vis0 = x.vis1 = x.vis2 = x.vis3 = 0;
+    x.mlay = FAR;
+    x.lastl = 65535;   // the static field holds every reachable cell
 }
 // scenario 0 contact, 1 approach, 2 mixed (fixture = world % 2, then (world*7)%32 warm-up
 // waits), as gpu-d1/src/bench.cu:151-166.
@@ -684,7 +696,7 @@ __global__ __launch_bounds__(64) void k_wait(uint8_t *worlds, int n, int count, 
     wait_stage_map(x, map);
     int fixture = 0;
     uint8_t *row = worlds + (size_t)w * WAIT_BYTES;
-    wait_load(x, row, count, fixture);
+    wait_load(x, map, row, count, fixture);
     for (int k = 0; k < steps; k++) {
         wait_step(x, map, count, fixture);
         if (trace) {

@@ -21,9 +21,10 @@
 // Task constants are those of gpu-d1/branches/d1-stairs-v2/scripts/assets.py:5.
 // D1_CLUMP_MODE (0 or 1) selects the reset's clumped placement, as the reference's
 // CLUMP_MODE build flag does.
-#include "d1_core.h"
-
 #include "../../include/d1learn.h"
+
+#define D1_STAGE_FLOATS D1L_OBS   // the fp32 observation is staged over the dead BFS bitmaps
+#include "d1_core.h"
 
 #ifndef D1_CLUMP_MODE
 #define D1_CLUMP_MODE 0
@@ -83,10 +84,6 @@ struct LCtx {
 };
 
 __device__ __forceinline__ Row row_xor(Row x, Row y) { return {x.a ^ y.a, x.b ^ y.b, x.c ^ y.c}; }
-__device__ __forceinline__ int wave_min(int v) {
-    for (int o = 32; o; o >>= 1) v = imin(v, __shfl_xor(v, o));
-    return uni(v);
-}
 __device__ __forceinline__ int lanes_below(uint64_t m, int lane) {
     return __popcll(m & ((1ULL << lane) - 1ULL));
 }
@@ -411,8 +408,8 @@ __device__ __forceinline__ void reset_learn(LCtx &c) {
 }
 
 // ---------------------------------------------------------------- known-floor BFS (learn.cu:222-266)
-// Bit-parallel BFS over viewed floor from the player into sm->dist (layer mod 256) /
-// sm->reach. Stops when the first layer holding an anchor is found (its anchors then
+// Bit-parallel BFS over viewed floor from the player into sm->reach and the layer-mod-3
+// planes sm->lay0/lay1. Stops when the first layer holding an anchor is found (its anchors then
 // replace L->anch), every wanted stair has a layer and every wanted monster lane is
 // reached, or nothing new is reached. Returns the anchor layer or -1.
 struct KB {
@@ -422,8 +419,8 @@ struct KB {
 };
 // Lane l keeps rows l and (l < 6) 64 + l of the frontier, reach, known floor and anchors in
 // registers; vertical neighbours arrive by lane shuffles, so a layer needs no LDS round
-// trip and no barrier. The layer of every reached cell is scattered into sm->dist as it is
-// reached; reach, the last layer's frontier and the anchor rows are published at the end.
+// trip and no barrier. Reach, the layer planes, the last layer's frontier and the anchor
+// rows are published at the end.
 __device__ __forceinline__ uint32_t row_word(Row r, int w) { return w == 0 ? r.a : w == 1 ? r.b : r.c; }
 __device__ __forceinline__ KB known_bfs(LCtx &c, bool want_anchor, int want_stairs, bool want_monster) {
     Ctx &x = c.x;
@@ -445,7 +442,8 @@ __device__ __forceinline__ KB known_bfs(LCtx &c, bool want_anchor, int want_stai
     const Row pbit = row_range(px, px);
     Row f0 = lane == py ? pbit : zero, f1 = has1 && 64 + lane == py ? pbit : zero;
     Row r0 = f0, r1 = f1;
-    if (lane == 0) sm->dist[x.player] = 0;
+    Row e0 = zero, e1 = zero, g0 = zero, g1 = zero;   // layer % 3 == 1, layer % 3 == 2
+    int m3 = 0;
     // wanted stairs: holder lane, register row and word of each (uniform)
     const int s0 = stair_at(x, 0), s1 = stair_at(x, 1), s2 = stair_at(x, 2);
     // this lane's monster cell, when it is wanted: holder lane and word of its row
@@ -462,14 +460,9 @@ __device__ __forceinline__ KB known_bfs(LCtx &c, bool want_anchor, int want_stai
             const Row n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), k1), r1) : zero;
             r0 = row_or(r0, n0); r1 = row_or(r1, n1);
             f0 = n0; f1 = n1;
-            scatter_layer(sm, lane * W, n0.a, layer);
-            scatter_layer(sm, lane * W + 32, n0.b, layer);
-            scatter_layer(sm, lane * W + 64, n0.c, layer);
-            if (has1) {
-                scatter_layer(sm, (64 + lane) * W, n1.a, layer);
-                scatter_layer(sm, (64 + lane) * W + 32, n1.b, layer);
-                scatter_layer(sm, (64 + lane) * W + 64, n1.c, layer);
-            }
+            m3 = m3 == 2 ? 0 : m3 + 1;
+            if (m3 == 1) { e0 = row_or(e0, n0); e1 = row_or(e1, n1); }
+            if (m3 == 2) { g0 = row_or(g0, n0); g1 = row_or(g1, n1); }
             if (!ballot(row_any(n0) || row_any(n1))) break;
         }
         bool done = true;
@@ -506,7 +499,12 @@ __device__ __forceinline__ KB known_bfs(LCtx &c, bool want_anchor, int want_stai
     }
     row_st(sm->reach, lane, r0);
     row_st(sm->front, lane, f0);
-    if (has1) { row_st(sm->reach, 64 + lane, r1); row_st(sm->front, 64 + lane, f1); }
+    row_st(sm->lay0, lane, e0);
+    row_st(sm->lay1, lane, g0);
+    if (has1) {
+        row_st(sm->reach, 64 + lane, r1); row_st(sm->front, 64 + lane, f1);
+        row_st(sm->lay0, 64 + lane, e1); row_st(sm->lay1, 64 + lane, g1);
+    }
     if (want_anchor) {   // the nearest layer's anchors; none reachable: the set is not needed
         row_st(L->anch, lane, r.alayer >= 0 ? a0 : zero);
         if (has1) row_st(L->anch, 64 + lane, r.alayer >= 0 ? a1 : zero);
@@ -515,7 +513,9 @@ __device__ __forceinline__ KB known_bfs(LCtx &c, bool want_anchor, int want_stai
     return r;
 }
 // route_first_step (learn.cu:248-264): back from target (at layer D) along the first
-// predecessor in direction order; the player's direction to the layer-1 cell.
+// predecessor in direction order; the player's direction to the layer-1 cell. A reached
+// neighbour of a layer-D cell is at layer D-1 exactly when its layer mod 3 is (D-1) mod 3
+// (neighbours differ by at most one layer).
 __device__ __forceinline__ int route_first_step(const LCtx &c, int target, int D) {
     const Ctx &x = c.x;
     const Smem *sm = x.sm;
@@ -523,7 +523,7 @@ __device__ __forceinline__ int route_first_step(const LCtx &c, int target, int D
     int p = target;
     for (; D > 1; D--) {
         int q = nbr(p, x.lane & 7);
-        bool ok = x.lane < 8 && q >= 0 && bit(sm->reach, q) && sm->dist[q] == (uint8_t)(D - 1);
+        bool ok = x.lane < 8 && q >= 0 && bit(sm->reach, q) && lay3(sm, q) == (D - 1) % 3;
         uint64_t mm = ballot(ok);
         if (!mm) return -1;
         p = lane_val(q, __ffsll((unsigned long long)mm) - 1);
@@ -744,7 +744,7 @@ __device__ __forceinline__ void observe_learn(LCtx &c, float *obs, float *mask) 
     const bool on_stair = stair_index(x) > 0;
     const bool rest_ok = x.hp < cf->hp && cf->regen > 0 && !visible_awake(x);
     __syncthreads();
-    float *ob = (float *)sm->dist;   // the BFS field is no longer needed
+    float *ob = sm->stage;   // overlays the BFS bitmaps, which are no longer needed
     for (int j = x.lane; j < D1L_OBS; j += 64) ob[j] = 0.f;
     __syncthreads();
     for (int w = x.lane; w < 225; w += 64) {
