@@ -680,8 +680,13 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
 // planes in registers; vertical neighbours arrive by DPP lane shifts, so a layer has no LDS
 // access and no barrier. Reach and the planes are published to LDS at the end (the monster
 // phase reads them); the frontier bitmap is left clear for the repair search's marks.
-__device__ __forceinline__ uint32_t lane_up(uint32_t v) { return (uint32_t)dpp<DPP_WAVE_SHR1>((int)v, 0); }   // lane l <- l-1
-__device__ __forceinline__ uint32_t lane_dn(uint32_t v) { return (uint32_t)dpp<DPP_WAVE_SHL1>((int)v, 0); }   // lane l <- l+1
+// lane l <- l-1 / l+1; bound control makes lane 0 / lane 63 (no source lane) read 0
+__device__ __forceinline__ uint32_t lane_up(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_WAVE_SHR1, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint32_t lane_dn(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_WAVE_SHL1, 0xF, 0xF, true);
+}
 __device__ __forceinline__ Row row_up(Row r) { return {lane_up(r.a), lane_up(r.b), lane_up(r.c)}; }
 __device__ __forceinline__ Row row_dn(Row r) { return {lane_dn(r.a), lane_dn(r.b), lane_dn(r.c)}; }
 __device__ __forceinline__ Row row_lane(Row r, int l) {

@@ -512,10 +512,9 @@ constexpr int STEP_TAIL = 8192;
 __host__ __device__ inline int step_pairs(int n) { return (n - (n < STEP_TAIL ? n : STEP_TAIL) + 1) / 2; }
 __host__ __device__ inline int step_blocks(int n) { const int b2 = step_pairs(n); return b2 + (n - 2 * b2); }
 template <int RM>
-__global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg,
-                                             D1Tables tab, const int64_t *actions, uint8_t *obs, float *out,
-                                             uint32_t *hash, const uint8_t *active) {
-    __shared__ Smem sm;
+__device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int max_m, size_t row_bytes,
+                                            const D1Config &cfg, const D1Tables &tab, const int64_t *actions,
+                                            uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     const int b2 = step_pairs(n), blk = (int)blockIdx.x;   // first < n for every block of step_blocks(n)
     const int first = blk < b2 ? 2 * blk : 2 * b2 + (blk - b2), last = imin(n, blk < b2 ? first + 2 : first + 1);
     Ctx x;
@@ -556,6 +555,27 @@ __global__ __launch_bounds__(64) void k_step(uint8_t *state, int n, int max_m, s
             if (x.lane == 0) hash[env] = h;
         }
     }
+}
+
+// Two builds of the same step. A world with at most 8 monsters spends its time in straight
+// issue-bound code (observation, reveal, scalar rules): 4 waves per SIMD without spills. The
+// crowded layouts (up to 64 monsters) spend it in serial monster turns whose LDS and
+// cross-lane latencies want more waves in flight: 6 waves per SIMD, which costs some
+// register spills (measured at 262,144 worlds x 40 monsters: 8.3 -> 7.0 ms per step; at
+// 65,536 x 8 the same build is 0.17 -> 0.33 ms, hence two builds).
+template <int RM>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_step(
+    uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
+    uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
+    __shared__ Smem sm;
+    step_worlds<RM>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
+}
+template <int RM>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_step_crowd(
+    uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
+    uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
+    __shared__ Smem sm;
+    step_worlds<RM>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
 }
 
 // ---------------------------------------------------------------- monster-wait workload
@@ -822,7 +842,8 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
     if (e) return e;
     if (!state || !actions) return D1_E_ARG;
     if (n == 0) return 0;
-    auto kern = cfg->rng_mode == 0 ? d1::k_step<0> : d1::k_step<1>;
+    auto kern = max_monsters > 8 ? (cfg->rng_mode == 0 ? d1::k_step_crowd<0> : d1::k_step_crowd<1>)
+                                 : (cfg->rng_mode == 0 ? d1::k_step<0> : d1::k_step<1>);
     hipLaunchKernelGGL(kern, dim3(d1::step_blocks(n)), dim3(64), 0, (hipStream_t)stream,
                        (uint8_t *)state, n, max_monsters,
                        (size_t)d1::state_bytes(max_monsters), *cfg, *tab, actions, obs, out, hash, active);
