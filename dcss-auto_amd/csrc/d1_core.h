@@ -315,6 +315,10 @@ struct Ctx {
     int mlay;    // absolute BFS layer of the monster's cell (FAR when not known)
     int lastl;   // last layer the field holds: a reached cell next to an unreached one is on it
     int lane;
+    // distance-field memo in the state row (crowded layouts): its address, the player cell the
+    // stored field belongs to (-1: none), and the player cell whose field LDS holds (-1: none)
+    uint32_t *fcache = nullptr;
+    int ftag = -1, fld = -1;
 };
 
 __device__ __forceinline__ int stair_at(const Ctx &x, int k) { return (int16_t)(uint16_t)(x.stairs >> (16 * k)); }

@@ -51,7 +51,15 @@ constexpr int OFF_VIEW = 64, OFF_MON = 96;
 __host__ __device__ constexpr int off_viewed(int m) { return OFF_MON + 8 * m; }
 __host__ __device__ constexpr int off_floor(int m) { return off_viewed(m) + ROWS_WORDS * 4; }
 __host__ __device__ constexpr int off_cells(int m) { return off_floor(m) + ROWS_WORDS * 4; }
-__host__ __device__ constexpr int state_bytes(int m) { return (off_cells(m) + ROWS_WORDS * 4 + 63) / 64 * 64; }
+// Layouts with more than 8 monsters also keep the distance-field memo: dword 0 the player
+// cell it was computed for (-1: none), dword 1 its last layer, dwords 2-33 the monsters'
+// absolute layers (int16 each, 32767 = unknown), then the reach, lay0 and lay1 bitmaps.
+constexpr int FC_HEAD = 34, FC_DWORDS = FC_HEAD + 3 * ROWS_WORDS;
+__host__ __device__ constexpr bool has_fcache(int m) { return m > 8; }
+__host__ __device__ constexpr int off_fcache(int m) { return off_cells(m) + ROWS_WORDS * 4; }
+__host__ __device__ constexpr int state_bytes(int m) {
+    return (off_fcache(m) + (has_fcache(m) ? FC_DWORDS * 4 : 0) + 63) / 64 * 64;
+}
 
 // ---------------------------------------------------------------- episode reset
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:351-446 (player, then monsters by
@@ -114,6 +122,39 @@ __device__ __forceinline__ void reset(Ctx &x, const uint32_t *cells_g) {
         __syncthreads();
     }
     reveal(x);
+    x.ftag = -1;   // a new player cell and new monster cells: the memo no longer applies
+    x.fld = -1;    // and the reach bitmap held the stairs' eligible cells
+}
+
+// ---------------------------------------------------------------- distance-field memo
+// The distance field is a function of the level and the player's cell only. The crowded
+// layouts keep a complete field (BFS to exhaustion, every living monster's layer recorded)
+// in the state row and reuse it while the player stays on that cell; monster moves keep
+// their layers exact (a move is to a reached neighbour, one of -1/0/+1 away). A step whose
+// player stands still then reads 2,520 bytes instead of running the whole BFS.
+__device__ __forceinline__ void field_memo(Ctx &x) {
+    if (x.fld == x.player) return;   // LDS holds it already (a REST repeat)
+    Smem *sm = x.sm;
+    uint32_t *fc = x.fcache;
+    if (x.ftag == x.player) {
+        for (int w = x.lane; w < ROWS_WORDS; w += 64) {
+            sm->reach[w] = fc[FC_HEAD + w];
+            sm->lay0[w] = fc[FC_HEAD + ROWS_WORDS + w];
+            sm->lay1[w] = fc[FC_HEAD + 2 * ROWS_WORDS + w];
+            sm->front[w] = 0;   // the repair search's queued marks start clear, as after bfs()
+        }
+        __syncthreads();
+    } else {
+        const uint64_t living = ballot(x.lane < x.c->count && x.mhp > 0);
+        bfs(x, living, BIG);
+        for (int w = x.lane; w < ROWS_WORDS; w += 64) {
+            fc[FC_HEAD + w] = sm->reach[w];
+            fc[FC_HEAD + ROWS_WORDS + w] = sm->lay0[w];
+            fc[FC_HEAD + 2 * ROWS_WORDS + w] = sm->lay1[w];
+        }
+        x.ftag = x.player;
+    }
+    x.fld = x.player;
 }
 
 // ---------------------------------------------------------------- one physical turn
@@ -168,7 +209,10 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
         for (int k = 0; k < 6; k++) maxspeed = imax(maxspeed, c->kinds[k].speed);
         x.menergy = (int16_t)x.menergy;
         uint64_t movers = ballot(mine && x.mhp > 0 && x.mawake && x.menergy >= 80 && cheb(x.mpos, x.player) > 1);
-        if (movers) bfs(x, movers, imax(2, (maxspeed + 9) / 10));
+        if (movers) {
+            if (x.fcache) field_memo(x);
+            else bfs(x, movers, imax(2, (maxspeed + 9) / 10));
+        }
         while (x.hp > 0) {
             int key = (mine && x.menergy >= 80) ? x.menergy * 128 + 127 - x.lane : -1;
             key = wave_max(key);
@@ -352,6 +396,11 @@ __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
     }
     uint32_t *vg = (uint32_t *)(row + off_viewed(max_m));
     for (int w = x.lane; w < ROWS_WORDS; w += 64) vg[w] = x.sm->viewed[w];
+    if (has_fcache(max_m)) {   // memo head: its player cell, last layer, the monsters' layers
+        uint32_t *fc = (uint32_t *)(row + off_fcache(max_m));
+        if (x.lane == 0) { fc[0] = (uint32_t)x.ftag; fc[1] = (uint32_t)x.lastl; }
+        if (x.lane < max_m) ((int16_t *)(fc + 2))[x.lane] = (int16_t)imin(x.mlay, 32767);
+    }
 }
 
 // ---------------------------------------------------------------- level generator
@@ -410,6 +459,7 @@ struct Pre {
     uint32_t hv;
     u32x2 mon;
     uint32_t vw[4], fl[4];
+    uint32_t fh;   // dword lane of the distance-field memo head (crowded layouts)
     int64_t act;
     int on;
 };
@@ -424,6 +474,7 @@ __device__ __forceinline__ void prefetch_world(Pre &pf, const uint8_t *row, int 
         pf.vw[i] = vg[w];
         pf.fl[i] = fg[w];
     }
+    pf.fh = has_fcache(max_m) ? ((const uint32_t *)(row + off_fcache(max_m)))[imin(lane, FC_HEAD - 1)] : 0u;
     pf.act = actions[env];
     pf.on = active ? active[env] : 1;
 }
@@ -448,6 +499,16 @@ __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
         x.menergy = (int16_t)(pf.mon.y & 0xFFFFu); x.mawake = (pf.mon.y >> 16) & 0xFFu; x.mkind = pf.mon.y >> 24;
     } else {
         x.mpos = -1; x.mhp = 0; x.menergy = -30000; x.mawake = 0; x.mkind = 0;
+    }
+    x.fld = -1;
+    if (has_fcache(max_m)) {
+        x.ftag = (int)__builtin_amdgcn_readlane((int)pf.fh, 0);
+        x.lastl = (int)__builtin_amdgcn_readlane((int)pf.fh, 1);
+        const uint32_t pair = (uint32_t)__shfl((int)pf.fh, 2 + (x.lane >> 1));
+        const int ml = (int16_t)(x.lane & 1 ? pair >> 16 : pair & 0xFFFFu);
+        x.mlay = ml >= 32767 ? FAR : ml;
+    } else {
+        x.ftag = -1;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -495,6 +556,7 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
     if (cfg.rng_mode == 0) x.g.pcg_seed(mix64(seed + (uint64_t)env), (uint64_t)env + 1);
     else x.g.counter(seed, (uint32_t)env, 0, 2);
     x.decisions = 0; x.floor_seen = 0;
+    x.mlay = FAR; x.lastl = 0;
     reset(x, cg);
     store_world(x, row, max_m);
     if (obs) write_obs(x, obs + (size_t)env * D1_OBS_BYTES);
@@ -536,6 +598,7 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
             continue;
         }
         unpack_world<RM>(x, pf, max_m);
+        x.fcache = has_fcache(max_m) ? (uint32_t *)(row + off_fcache(max_m)) : nullptr;
         const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
         const int action = a < 0 || a > 1000 ? -1 : (int)a;
         float o8[8];

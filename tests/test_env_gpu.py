@@ -78,3 +78,21 @@ def test_step_without_hash_is_the_same_step(pkg):
     torch.cuda.synchronize()
     assert torch.equal(a.state, b.state) and torch.equal(a.obs, b.obs) and torch.equal(a.out, b.out)
     assert torch.equal(b.hash, h0)
+
+
+def test_crowded_field_memo_standing_player(pkg):
+    """The crowded layouts reuse the stored distance field while the player stands still.
+    40-monster worlds (half awake) driven mostly by WAIT and REST, with a move or an attack
+    now and then, so most steps reload the stored field (and every move recomputes it):
+    state hash, out[] and the observation equal the oracle's every step."""
+    print('[parity] crowded field memo', flush=True)
+    cfg = pkg.stress_config()
+    n = 96
+    gpu = pkg.Env(n, cfg, seed=13)
+    cpu = O.OracleEnv(n, cfg, seed=13, threads=8)
+    rng = np.random.default_rng(3)
+    for k in range(160):
+        a = np.where(rng.random(n) < 0.85, rng.choice([16, 17], n), rng.integers(0, 16, n)).astype(np.int64)
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, 'crowded memo')
