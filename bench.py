@@ -286,7 +286,7 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
     wall = time.perf_counter() - t0
     step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
     achieved = STEP_BYTES[40] * envs / (step_ms * 1e-3) / 1e9
-    traffic = measured_traffic(ROOT / 'profiles' / 'k_step_c5_hbm_traffic.md')
+    traffic = measured_traffic(ROOT / 'profiles' / 'k_step_c5_counters.md')
     return {'metric': 'env decisions/sec at 262,144 envs, 40 monsters, AR 8x25 head (C5)',
             'value': envs * horizon / wall, 'unit': 'decisions/s', 'n_gpus': 1, 'higher_is_better': True,
             'ms_per_step': wall / horizon * 1e3,
