@@ -29,7 +29,7 @@ class D1PPOStep(C.Structure):
                 ('off_w3', C.c_int64), ('off_b3', C.c_int64), ('step', C.c_void_p), ('loss_parts', C.c_void_p), ('work', C.c_void_p),
                 ('work_bytes', C.c_int64), ('clip', C.c_float), ('vcoef', C.c_float), ('ecoef', C.c_float),
                 ('max_grad_norm', C.c_float), ('lr', C.c_float), ('beta1', C.c_float), ('beta2', C.c_float),
-                ('eps', C.c_float)]
+                ('eps', C.c_float), ('z_out', C.c_void_p)]
 
 
 def load():

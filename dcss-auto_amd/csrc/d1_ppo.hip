@@ -46,8 +46,8 @@ constexpr int BP = 544;               // bias partial row: db1[256] | db2[256] |
 constexpr int C1 = 29;                // layer-1 K chunks (28 of 64 + the 8 inputs 1792..1799)
 constexpr int XB = 57;                // 32-row blocks of the x copy (1824 rows, 1800..1823 zero)
 constexpr int KW = 1024;              // samples per dW1 / dW2 workgroup
-constexpr int KW2 = 512;              // samples per dW3 workgroup
-constexpr int NT1 = 29;               // dW1 column tiles of 64 (the last one holds 8 columns)
+constexpr int KW3 = 256;              // samples per dW3 / dW1-tail slice (one per dW2 workgroup)
+constexpr int NT1 = 28;               // dW1 column tiles of 64 (inputs 0..1791; 1792..1799 are the tail)
 constexpr int NRED = (H * K1 + H * H + NZ * H) / 4 / 256 + 1;   // k_reduce weight workgroups: one unit per lane
 constexpr int NBIASB = (2 * H + NZ + 7) / 8;     // k_reduce bias workgroups (8 columns x 32 lanes each)
 
@@ -65,7 +65,8 @@ struct Work {
     uint16_t *dzf;                       // [32 rows (17 used)][mb] bf16, fragment order
     uint8_t *xf;                         // [1824 rows][mb] uint8 x^T, 16-byte fragment order
     float *bpart;                        // [mb/32][BP]
-    float *part1, *part2, *part3;        // [mb/KW][256][1800], [mb/KW][256][256], [mb/KW2][17][256]
+    float *part1, *part2, *part3;        // [mb/KW][256][1800] (columns < 1792), [mb/KW][256][256], [mb/KW3][17][256]
+    float *part1t;                       // [mb/KW3][256][8]: dW1 columns 1792..1799
     float *npart;                        // [NRED + NBIASB] sum-of-squares partials
 };
 
@@ -291,6 +292,10 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         for (int q = 1; q < 8; q++) zj += zp[q][r][j], zv += zp[q][r][NA];
         const float l = bf(rb(zj + bf(B3[j])));         // the head output is bf16
         const float value = bf(rb(zv + bf(B3[NA])));
+        if (a.z_out) {
+            a.z_out[(size_t)(m0 + r) * NZ + j] = l;
+            if (j == 0) a.z_out[(size_t)(m0 + r) * NZ + NA] = value;
+        }
         float mx = l;
 #pragma unroll
         for (int o = 8; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
@@ -533,11 +538,13 @@ __device__ __forceinline__ void wgrad_tile2(const uint16_t *at, const void *bt, 
     }
 }
 
-// Grouped launch: [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW][dW3: mb/KW2].
-// dW1[n1][f] = sum_m dh1[m][n1] x[m][f]; dW2[n2][n1] = sum_m dh2[m][n2] h1[m][n1];
-// dW3[j][n] = sum_m dz[m][j] h2[m][n]. Each writes fp32 partials [split][rows][cols]. The
-// dW1 splits of one column tile are consecutive blocks, which a launch spreads over the
-// eight XCDs, so each XCD's L2 serves one sample range of dh1 to every column tile.
+// Grouped launch of 32 * mb/KW workgroups (one per CU at mb = 8192):
+// [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW splits, each also
+// taking one mb/KW3 slice of dW3 and of the dW1 tail]. dW1[n1][f] = sum_m dh1[m][n1] x[m][f];
+// dW2[n2][n1] = sum_m dh2[m][n2] h1[m][n1]; dW3[j][n] = sum_m dz[m][j] h2[m][n]. Each writes
+// fp32 partials [split][rows][cols]. The dW1 splits of one column tile are consecutive
+// blocks, which a launch spreads over the eight XCDs, so each XCD's L2 serves one sample
+// range of dh1 to every column tile.
 __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
     __shared__ uint4 bl[2 * 2 * 4 * 64];
     if (!cursor_ok(a)) return;
@@ -552,17 +559,15 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
             const int f = 64 * tile + 32 * bb + lr;
-            if (f < K1) {
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * K1 + f] = acc[i][bb][r];
-            }
+                for (int r = 0; r < 16; r++) out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * K1 + f] = acc[i][bb][r];
         }
         return;
     }
     b -= NT1 * s1;
-    if (b < 4 * s1) {
+    {
         const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
         wgrad_tile2<false>(w.dh2f, w.h1f, 2 * tile, 8, nch, split * (KW / 64), KW / 64, bl, acc);
@@ -574,19 +579,32 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
 #pragma unroll
                 for (int r = 0; r < 16; r++)
                     out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * H + 64 * tile + 32 * bb + lr] = acc[i][bb][r];
-        return;
     }
-    b -= 4 * s1;
-    floatx16 acc[1][2] = {};
-    wgrad_tile<1, 2, false, 3>(w.dzf, 0, 1, w.h2f, 2 * wave, 8, nch, b * (KW2 / 64), KW2 / 64, acc);
-    float *out = w.part3 + (size_t)b * NZ * H;
+    // slice b of dW3 (wave w: columns 64w..64w+63) and of the dW1 tail (wave w: rows
+    // 64w..64w+63 against x^T block 56, inputs 1792..1823, of which 1792..1799 are kept)
+    {
+        floatx16 acc[1][2] = {};
+        wgrad_tile<1, 2, false, 3>(w.dzf, 0, 1, w.h2f, 2 * wave, 8, nch, b * (KW3 / 64), KW3 / 64, acc);
+        float *out = w.part3 + (size_t)b * NZ * H;
 #pragma unroll
-    for (int bb = 0; bb < 2; bb++)
+        for (int bb = 0; bb < 2; bb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int j = drow(r, lh);
-            if (j < NZ) out[(size_t)j * H + 64 * wave + 32 * bb + lr] = acc[0][bb][r];
+            for (int r = 0; r < 16; r++) {
+                const int j = drow(r, lh);
+                if (j < NZ) out[(size_t)j * H + 64 * wave + 32 * bb + lr] = acc[0][bb][r];
+            }
+    }
+    {
+        floatx16 acc[2][1] = {};
+        wgrad_tile<2, 1, true, 3>(w.dh1f, 2 * wave, 8, w.xf, K1 / 32, XB, nch, b * (KW3 / 64), KW3 / 64, acc);
+        float *out = w.part1t + (size_t)b * H * 8;
+        if (lr < 8) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * 8 + lr] = acc[i][0][r];
         }
+    }
 }
 
 // ---------------------------------------------------------------- k_reduce
@@ -608,7 +626,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
         if (ok) a.step[1] = a.step[0] + 1.f;
     }
     if (!ok) return;
-    const int t = threadIdx.x, mb = a.mb, s1 = mb / KW, s2 = mb / KW2;
+    const int t = threadIdx.x, mb = a.mb, s1 = mb / KW, s3 = mb / KW3;
     uint16_t *g = (uint16_t *)a.g;
     float sq = 0.f;
     if (blockIdx.x < NRED) {
@@ -619,13 +637,18 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
             size_t stride;
             uint16_t *dst;
             if (u < U1) {
-                src = w.part1 + 4 * (size_t)u, S = s1, stride = (size_t)H * K1, dst = g + a.off_w1 + 4 * (size_t)u;
+                const int n = 4 * u / K1, f = 4 * u - n * K1;   // four inputs of one row (K1 % 4 == 0)
+                if (f < NT1 * 64)
+                    src = w.part1 + 4 * (size_t)u, S = s1, stride = (size_t)H * K1;
+                else
+                    src = w.part1t + (size_t)n * 8 + (f - NT1 * 64), S = s3, stride = (size_t)H * 8;
+                dst = g + a.off_w1 + 4 * (size_t)u;
             } else if (u < U1 + U2) {
                 const int e = u - U1;
                 src = w.part2 + 4 * e, S = s1, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
             } else {
                 const int e = u - U1 - U2;
-                src = w.part3 + 4 * e, S = s2, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
+                src = w.part3 + 4 * e, S = s3, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
             }
             float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
             for (int q0 = 0; q0 < S; q0 += 8) {   // eight loads in flight, summed in split order
@@ -780,7 +803,7 @@ __global__ __launch_bounds__(256) void k_pack(D1PPOStep a, uint16_t *wpk) {
 }
 
 struct Layout {
-    size_t wpk, h1f, h2f, dh2f, dh1f, dzf, xf, bpart, part1, part2, part3, npart, total;
+    size_t wpk, h1f, h2f, dh2f, dh1f, dzf, xf, bpart, part1, part2, part3, part1t, npart, total;
 };
 constexpr size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 constexpr Layout layout(int mb) {
@@ -796,7 +819,8 @@ constexpr Layout layout(int mb) {
     L.bpart = off, off += round256((size_t)(mb / R) * BP * 4);
     L.part1 = off, off += round256((size_t)(mb / KW) * H * K1 * 4);
     L.part2 = off, off += round256((size_t)(mb / KW) * H * H * 4);
-    L.part3 = off, off += round256((size_t)(mb / KW2) * NZ * H * 4);
+    L.part3 = off, off += round256((size_t)(mb / KW3) * NZ * H * 4);
+    L.part1t = off, off += round256((size_t)(mb / KW3) * H * 8 * 4);
     L.npart = off, off += round256((size_t)(NRED + NBIASB) * 4);
     L.total = off;
     return L;
@@ -830,6 +854,7 @@ static int check_args(const D1PPOStep *s, char *base, int64_t bytes, Work *w) {
     w->part1 = (float *)(base + L.part1);
     w->part2 = (float *)(base + L.part2);
     w->part3 = (float *)(base + L.part3);
+    w->part1t = (float *)(base + L.part1t);
     w->npart = (float *)(base + L.npart);
     return 0;
 }
@@ -843,9 +868,9 @@ static void launch_pack(const D1PPOStep &a, const Work &w, hipStream_t st) {
     hipLaunchKernelGGL(k_pack, dim3(512), dim3(256), 0, st, a, w.wpk);
 }
 static void launch_step(const D1PPOStep &a, const Work &w, hipStream_t st) {
-    const int s1 = a.mb / KW, s2 = a.mb / KW2;
+    const int s1 = a.mb / KW;
     hipLaunchKernelGGL(k_rows, dim3(a.mb / R), dim3(512), 0, st, a, w);
-    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1 + s2), dim3(256), 0, st, a, w);
+    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1), dim3(256), 0, st, a, w);
     hipLaunchKernelGGL(k_reduce, dim3(NRED + NBIASB), dim3(256), 0, st, a, w);
     const int64_t nadam = (a.nparams / 4 + 255) / 256;   // one group of four parameters per lane
     hipLaunchKernelGGL(k_adam, dim3((unsigned)nadam), dim3(256), 0, st, a, w);

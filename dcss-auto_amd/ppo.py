@@ -149,6 +149,7 @@ class FastPPO:
         _lib.check(0 if nbytes > 0 else nbytes, 'd1_ppo_work_bytes')
         self.work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         self.perm = None
+        self.head_out = None   # [minibatch, 17] fp32: when set, each step writes its head outputs here
         self._packed = False
         self._g = self._g_buf = None
         self._args = self._args_key = None
@@ -156,7 +157,7 @@ class FastPPO:
     def _struct(self, obs, actions, logp, adv, ret):
         from . import _lib
         key = (obs.data_ptr(), actions.data_ptr(), logp.data_ptr(), adv.data_ptr(), ret.data_ptr(),
-               self.perm.data_ptr(), obs.shape[0])
+               self.perm.data_ptr(), obs.shape[0], 0 if self.head_out is None else self.head_out.data_ptr())
         if self._args_key != key:
             F = self.flat
             if obs.shape[1] != OBS or not obs.is_contiguous() or obs.dtype != torch.uint8:
@@ -170,13 +171,20 @@ class FastPPO:
                 off_w2=off['l2.weight'], off_b2=off['l2.bias'], off_w3=off['head.weight'],
                 off_b3=off['head.bias'], step=self.step_t.data_ptr(), loss_parts=self.loss_parts.data_ptr(), work=self.work.data_ptr(),
                 work_bytes=self.work.numel(), clip=self.clip, vcoef=self.vcoef, ecoef=self.ecoef,
-                max_grad_norm=self.max_grad_norm, lr=self.lr, beta1=0.9, beta2=0.999, eps=self.eps)
+                max_grad_norm=self.max_grad_norm, lr=self.lr, beta1=0.9, beta2=0.999, eps=self.eps,
+                z_out=None if self.head_out is None else self.head_out.data_ptr())
             self._args_key = key
         if not self._packed:   # kernel-ordered weight copies in the work buffer, from pb
             _lib.check(_lib.load().d1_ppo_prepare(self._args, torch.cuda.current_stream(self.dev).cuda_stream),
                        'd1_ppo_prepare')
             self._packed = True
         return self._args
+
+    def record_head(self, on=True):
+        """Have every following minibatch step write the head outputs its loss was computed
+        from (16 logits + value, bf16-rounded, as fp32) into self.head_out [minibatch, 17].
+        Steps already captured in a graph keep the setting they were captured with."""
+        self.head_out = torch.empty((self.minibatch, 17), dtype=torch.float32, device=self.dev) if on else None
 
     def set_order(self, perm):
         """Sample order of the next minibatches (int64 [n] on the device); resets the cursor

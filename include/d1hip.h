@@ -241,6 +241,9 @@ typedef struct {
     void *work;                     /* d1_ppo_work_bytes(mb) bytes of device memory, 256-byte aligned */
     int64_t work_bytes;
     float clip, vcoef, ecoef, max_grad_norm, lr, beta1, beta2, eps;
+    float *z_out;                   /* optional [mb, 17]: the head outputs the loss was computed from (16 logits
+                                       and the value, each the bf16-rounded head output widened to fp32), in
+                                       minibatch order; null to skip */
 } D1PPOStep;
 int64_t d1_ppo_work_bytes(int mb);
 int d1_ppo_prepare(const D1PPOStep *s, void *stream);
@@ -250,7 +253,7 @@ int d1_ppo_step(const D1PPOStep *s, void *stream);
  * under graph capture, tight serving loops, harnesses that forbid hipMalloc): d1_ppo_step
  * with the work buffer owned by the library, so s->work and s->work_bytes are ignored.
  * The buffer is one file-scope device array per GPU of d1_ppo_work_bytes(D1_PPO_STATIC_MAX_MB)
- * bytes (51,169,792), held from the library's load until the process ends; a larger s->mb
+ * bytes (51,710,464), held from the library's load until the process ends; a larger s->mb
  * returns D1_E_SCRATCH. Each call first rebuilds the packed
  * weight copies from s->pb (as d1_ppo_prepare does) and then runs d1_ppo_step's kernels, so
  * one call equals d1_ppo_prepare + d1_ppo_step on a private work buffer, bit for bit.
