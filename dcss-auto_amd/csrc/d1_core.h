@@ -319,6 +319,9 @@ struct Ctx {
     // stored field belongs to (-1: none), and the player cell whose field LDS holds (-1: none)
     uint32_t *fcache = nullptr;
     int ftag = -1, fld = -1;
+    // rows of the viewed bitmap changed since the world was loaded (vlo > vhi: none); the
+    // default, every row, is what a world that was not loaded from a state row writes back
+    int vlo = 0, vhi = H - 1;
 };
 
 __device__ __forceinline__ int stair_at(const Ctx &x, int k) { return (int16_t)(uint16_t)(x.stairs >> (16 * k)); }
@@ -426,6 +429,8 @@ __device__ __forceinline__ int reveal(Ctx &x) {
     __syncthreads();
     if (mine) row_st(x.sm->viewed, y, row_or(mask, row_ld(x.sm->viewed, y)));
     __syncthreads();
+    x.vlo = imin(x.vlo, imax(py - 7, 0));
+    x.vhi = imax(x.vhi, imin(py + 7, H - 1));
     int total = (int)wave_sum((uint32_t)fresh);
     x.floor_seen += total;
     return total;

@@ -70,6 +70,7 @@ __device__ __forceinline__ void reset(Ctx &x, const uint32_t *cells_g) {
     Smem *sm = x.sm;
     const D1Config *c = x.c;
     for (int w = x.lane; w < ROWS_WORDS; w += 64) { sm->occ[w] = 0; sm->front[w] = cells_g[w]; sm->viewed[w] = 0; }
+    x.vlo = 0, x.vhi = H - 1;
     __syncthreads();
     x.ncells = row_prefix(x, sm->front);
     x.player = select_cell(x, sm->front, x.g.r(x.ncells));
@@ -394,8 +395,10 @@ __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
         uint64_t v = x.lane == 0 ? x.vis0 : x.lane == 1 ? x.vis1 : x.lane == 2 ? x.vis2 : x.vis3;
         ((uint64_t *)(row + OFF_VIEW))[x.lane] = v;
     }
+    // the viewed rows this step changed: the reveal bands of the cells the player moved to,
+    // every row after a reset, none when the player did not move
     uint32_t *vg = (uint32_t *)(row + off_viewed(max_m));
-    for (int w = x.lane; w < ROWS_WORDS; w += 64) vg[w] = x.sm->viewed[w];
+    for (int w = RW * x.vlo + x.lane; w < RW * (x.vhi + 1); w += 64) vg[w] = x.sm->viewed[w];
     if (has_fcache(max_m)) {   // memo head: its player cell, last layer, the monsters' layers
         uint32_t *fc = (uint32_t *)(row + off_fcache(max_m));
         if (x.lane == 0) { fc[0] = (uint32_t)x.ftag; fc[1] = (uint32_t)x.lastl; }
@@ -501,6 +504,7 @@ __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
         x.mpos = -1; x.mhp = 0; x.menergy = -30000; x.mawake = 0; x.mkind = 0;
     }
     x.fld = -1;
+    x.vlo = H, x.vhi = -1;   // no viewed row changed yet
     if (has_fcache(max_m)) {
         x.ftag = (int)__builtin_amdgcn_readlane((int)pf.fh, 0);
         x.lastl = (int)__builtin_amdgcn_readlane((int)pf.fh, 1);
