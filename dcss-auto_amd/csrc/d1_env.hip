@@ -570,19 +570,22 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
     }
 }
 
-// Worlds per k_step workgroup: two (the second world's loads overlap the first's stores),
-// except the last STEP_TAIL worlds, one per workgroup: the workgroups dispatched last then
-// hold one world, not two, which shortens the tail in which a few slow worlds (resets,
-// long monster turns) run on an otherwise idle chip (k_step 193 -> 187 us at 65,536 worlds).
-constexpr int STEP_TAIL = 8192;
-__host__ __device__ inline int step_pairs(int n) { return (n - (n < STEP_TAIL ? n : STEP_TAIL) + 1) / 2; }
-__host__ __device__ inline int step_blocks(int n) { const int b2 = step_pairs(n); return b2 + (n - 2 * b2); }
-template <int RM>
+// Worlds per k_step workgroup: WPB consecutive worlds (each next world's loads overlap the
+// current one's stores and observation, so only a group's first load waits), except the
+// last STEP_TAIL worlds, one per workgroup: the workgroups dispatched last then hold one
+// world, which shortens the tail in which a few slow worlds (resets, long monster turns)
+// run on an otherwise idle chip (k_step 193 -> 187 us at 65,536 worlds). WPB is 4 for the
+// <= 8 monster build (0.176 -> 0.171 ms at 65,536 worlds) and 2 for the crowded build,
+// whose long serial worlds gain nothing from it.
+constexpr int STEP_TAIL = 8192, STEP_WPB = 4, CROWD_WPB = 2;
+__host__ __device__ inline int step_groups(int n, int wpb) { return (n - (n < STEP_TAIL ? n : STEP_TAIL)) / wpb; }
+__host__ __device__ inline int step_blocks(int n, int wpb) { const int g = step_groups(n, wpb); return g + (n - wpb * g); }
+template <int RM, int WPB>
 __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int max_m, size_t row_bytes,
                                             const D1Config &cfg, const D1Tables &tab, const int64_t *actions,
                                             uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
-    const int b2 = step_pairs(n), blk = (int)blockIdx.x;   // first < n for every block of step_blocks(n)
-    const int first = blk < b2 ? 2 * blk : 2 * b2 + (blk - b2), last = imin(n, blk < b2 ? first + 2 : first + 1);
+    const int g = step_groups(n, WPB), blk = (int)blockIdx.x;   // first < n for every block of step_blocks(n, WPB)
+    const int first = blk < g ? WPB * blk : WPB * g + (blk - g), last = imin(n, blk < g ? first + WPB : first + 1);
     Ctx x;
     x.sm = &sm; x.c = &cfg; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
     Pre pf;
@@ -635,14 +638,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
     uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
-    step_worlds<RM>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
+    step_worlds<RM, STEP_WPB>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
 }
 template <int RM>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_step_crowd(
     uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
     uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
-    step_worlds<RM>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
+    step_worlds<RM, CROWD_WPB>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
 }
 
 // ---------------------------------------------------------------- monster-wait workload
@@ -911,7 +914,8 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
     if (n == 0) return 0;
     auto kern = max_monsters > 8 ? (cfg->rng_mode == 0 ? d1::k_step_crowd<0> : d1::k_step_crowd<1>)
                                  : (cfg->rng_mode == 0 ? d1::k_step<0> : d1::k_step<1>);
-    hipLaunchKernelGGL(kern, dim3(d1::step_blocks(n)), dim3(64), 0, (hipStream_t)stream,
+    const int wpb = max_monsters > 8 ? d1::CROWD_WPB : d1::STEP_WPB;
+    hipLaunchKernelGGL(kern, dim3(d1::step_blocks(n, wpb)), dim3(64), 0, (hipStream_t)stream,
                        (uint8_t *)state, n, max_monsters,
                        (size_t)d1::state_bytes(max_monsters), *cfg, *tab, actions, obs, out, hash, active);
     return (int)hipGetLastError();
