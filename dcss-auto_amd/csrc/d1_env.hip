@@ -582,12 +582,12 @@ __host__ __device__ inline int step_groups(int n, int wpb) { return (n - (n < ST
 __host__ __device__ inline int step_blocks(int n, int wpb) { const int g = step_groups(n, wpb); return g + (n - wpb * g); }
 template <int RM, int WPB>
 __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int max_m, size_t row_bytes,
-                                            const D1Config &cfg, const D1Tables &tab, const int64_t *actions,
+                                            const D1Config *cfgp, const D1Tables &tab, const int64_t *actions,
                                             uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     const int g = step_groups(n, WPB), blk = (int)blockIdx.x;   // first < n for every block of step_blocks(n, WPB)
     const int first = blk < g ? WPB * blk : WPB * g + (blk - g), last = imin(n, blk < g ? first + WPB : first + 1);
     Ctx x;
-    x.sm = &sm; x.c = &cfg; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
+    x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
     Pre pf;
     prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
     for (int env = first; env < last; env++) {
@@ -632,20 +632,26 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
 // crowded layouts (up to 64 monsters) spend it in serial monster turns whose LDS and
 // cross-lane latencies want more waves in flight: 6 waves per SIMD, which costs some
 // register spills (measured at 262,144 worlds x 40 monsters: 8.3 -> 7.0 ms per step; at
-// 65,536 x 8 the same build is 0.17 -> 0.33 ms, hence two builds).
+// 65,536 x 8 the same build is 0.17 -> 0.33 ms, hence two builds). The <= 8 monster build
+// reads its configuration from an LDS copy, which keeps the fields out of scalar registers
+// (190 -> 104 spilled to VGPR lanes; 0.171 -> 0.168 ms at 65,536 worlds); in the crowded
+// build the same copy costs 4.69 -> 5.19 ms, so it reads the kernel argument.
 template <int RM>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_step(
     uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
     uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
-    step_worlds<RM, STEP_WPB>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
+    __shared__ D1Config lcfg;
+    for (int i = lane_id(); i < (int)(sizeof(D1Config) / 4); i += 64) ((uint32_t *)&lcfg)[i] = ((const uint32_t *)&cfg)[i];
+    __syncthreads();
+    step_worlds<RM, STEP_WPB>(sm, state, n, max_m, row_bytes, &lcfg, tab, actions, obs, out, hash, active);
 }
 template <int RM>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_step_crowd(
     uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
     uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
-    step_worlds<RM, CROWD_WPB>(sm, state, n, max_m, row_bytes, cfg, tab, actions, obs, out, hash, active);
+    step_worlds<RM, CROWD_WPB>(sm, state, n, max_m, row_bytes, &cfg, tab, actions, obs, out, hash, active);
 }
 
 // ---------------------------------------------------------------- monster-wait workload
