@@ -48,7 +48,12 @@ constexpr int XB = 57;                // 32-row blocks of the x copy (1824 rows,
 constexpr int KW = 1024;              // samples per dW1 / dW2 workgroup
 constexpr int KW3 = 256;              // samples per dW3 / dW1-tail slice (one per dW2 workgroup)
 constexpr int NT1 = 28;               // dW1 column tiles of 64 (inputs 0..1791; 1792..1799 are the tail)
-constexpr int NRED = (H * K1 + H * H + NZ * H) / 4 / 256 + 1;   // k_reduce weight workgroups: one unit per lane
+constexpr int NRF = (H * NT1 * 64 + H * H) / 4 / 256;   // k_reduce workgroups of mb/KW-partial units (dW1 columns
+                                                       // < 1792, dW2), one unit of four elements per lane
+constexpr int NRS = (H * 2 + NZ * H / 4) * 4 / 256;    // k_reduce workgroups of mb/KW3-partial units (dW1 columns
+                                                       // 1792..1799, dW3), four lanes per unit
+constexpr int NRED = NRF + NRS;
+static_assert((H * NT1 * 64 + H * H) % 1024 == 0 && (H * 2 + NZ * H / 4) * 4 % 256 == 0, "k_reduce unit split");
 constexpr int NBIASB = (2 * H + NZ + 7) / 8;     // k_reduce bias workgroups (8 columns x 32 lanes each)
 
 // packed weight copies (bf16 elements), all in fragment order
@@ -618,6 +623,28 @@ __device__ __forceinline__ float block_sum(float x, float *red) {   // 256 lanes
     return s;
 }
 
+// Sum of S partials (stride apart) of four elements, in partial order, eight loads in flight.
+__device__ __forceinline__ float4 sum_parts(const float *src, size_t stride, int S) {
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q0 = 0; q0 < S; q0 += 8) {
+        float4 x[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            x[j] = q0 + j < S ? *(const float4 *)(src + (q0 + j) * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < 8; j++) s.x += x[j].x, s.y += x[j].y, s.z += x[j].z, s.w += x[j].w;
+    }
+    return s;
+}
+// Four gradient elements -> bf16 at dst; returns the sum of squares of the rounded values.
+__device__ __forceinline__ float store_grad4(uint16_t *dst, float4 s) {
+    const uint32_t w01 = cvt2(s.x, s.y), w23 = cvt2(s.z, s.w);
+    *(uint2 *)dst = make_uint2(w01, w23);
+    const float h0 = __uint_as_float(w01 << 16), h1 = __uint_as_float(w01 & 0xFFFF0000u);
+    const float h2 = __uint_as_float(w23 << 16), h3 = __uint_as_float(w23 & 0xFFFF0000u);
+    return h0 * h0 + h1 * h1 + h2 * h2 + h3 * h3;
+}
+
 __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
     __shared__ float red[256];
     const bool ok = cursor_ok(a);
@@ -626,44 +653,47 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
         if (ok) a.step[1] = a.step[0] + 1.f;
     }
     if (!ok) return;
-    const int t = threadIdx.x, mb = a.mb, s1 = mb / KW, s3 = mb / KW3;
+    const int t = threadIdx.x, mb = a.mb, s1 = mb / KW;
     uint16_t *g = (uint16_t *)a.g;
     float sq = 0.f;
-    if (blockIdx.x < NRED) {
-        constexpr int U1 = H * K1 / 4, U2 = H * H / 4, U3 = NZ * H / 4;
-        for (int u = blockIdx.x * 256 + t; u < U1 + U2 + U3; u += NRED * 256) {
-            const float *src;
-            int S;
-            size_t stride;
-            uint16_t *dst;
-            if (u < U1) {
-                const int n = 4 * u / K1, f = 4 * u - n * K1;   // four inputs of one row (K1 % 4 == 0)
-                if (f < NT1 * 64)
-                    src = w.part1 + 4 * (size_t)u, S = s1, stride = (size_t)H * K1;
-                else
-                    src = w.part1t + (size_t)n * 8 + (f - NT1 * 64), S = s3, stride = (size_t)H * 8;
-                dst = g + a.off_w1 + 4 * (size_t)u;
-            } else if (u < U1 + U2) {
-                const int e = u - U1;
-                src = w.part2 + 4 * e, S = s1, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
-            } else {
-                const int e = u - U1 - U2;
-                src = w.part3 + 4 * e, S = s3, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
-            }
-            float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int q0 = 0; q0 < S; q0 += 8) {   // eight loads in flight, summed in split order
-                float4 x[8];
+    if (blockIdx.x < NRF) {   // s1 partials per unit, summed in split order
+        const int u = blockIdx.x * 256 + t;
+        const float *src;
+        size_t stride;
+        uint16_t *dst;
+        if (u < H * NT1 * 16) {
+            const int n = u / (NT1 * 16), f = 4 * (u - n * NT1 * 16);
+            src = w.part1 + (size_t)n * K1 + f, stride = (size_t)H * K1, dst = g + a.off_w1 + (size_t)n * K1 + f;
+        } else {
+            const int e = u - H * NT1 * 16;
+            src = w.part2 + 4 * e, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
+        }
+        const float4 s = sum_parts(src, stride, s1);
+        sq = store_grad4(dst, s);
+    } else if (blockIdx.x < NRED) {
+        // s3 = 4 s1 partials per unit: lane q of a quad sums partials q s1 .. q s1 + s1 - 1 in
+        // split order (all of a lane's loads in flight at once), the quad adds its four sums in
+        // order; 1,600 units (dW1 columns 1792..1799, then dW3) in 25 workgroups
+        const int vu = (blockIdx.x - NRF) * 64 + (t >> 2), q = t & 3;
+        const float *src;
+        size_t stride;
+        uint16_t *dst;
+        if (vu < 2 * H) {
+            const int n = vu >> 1, f = NT1 * 64 + 4 * (vu & 1);
+            src = w.part1t + (size_t)n * 8 + (f - NT1 * 64), stride = (size_t)H * 8, dst = g + a.off_w1 + (size_t)n * K1 + f;
+        } else {
+            const int e = vu - 2 * H;
+            src = w.part3 + 4 * e, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
+        }
+        const float4 s = sum_parts(src + (size_t)q * s1 * stride, stride, s1);
+        float4 o[3];
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    x[j] = q0 + j < S ? *(const float4 *)(src + (q0 + j) * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int j = 0; j < 8; j++) s.x += x[j].x, s.y += x[j].y, s.z += x[j].z, s.w += x[j].w;
-            }
-            const uint32_t w01 = cvt2(s.x, s.y), w23 = cvt2(s.z, s.w);
-            *(uint2 *)dst = make_uint2(w01, w23);
-            const float h0 = __uint_as_float(w01 << 16), h1 = __uint_as_float(w01 & 0xFFFF0000u);
-            const float h2 = __uint_as_float(w23 << 16), h3 = __uint_as_float(w23 & 0xFFFF0000u);
-            sq += h0 * h0 + h1 * h1 + h2 * h2 + h3 * h3;
+        for (int k = 0; k < 3; k++)
+            o[k] = make_float4(__shfl_down(s.x, k + 1), __shfl_down(s.y, k + 1), __shfl_down(s.z, k + 1), __shfl_down(s.w, k + 1));
+        if (q == 0) {
+            const float4 tot = make_float4(((s.x + o[0].x) + o[1].x) + o[2].x, ((s.y + o[0].y) + o[1].y) + o[2].y,
+                                           ((s.z + o[0].z) + o[1].z) + o[2].z, ((s.w + o[0].w) + o[1].w) + o[2].w);
+            sq = store_grad4(dst, tot);
         }
     } else {   // biases: 8 columns per workgroup, 32 lanes per column over the row partials
         const int col = 8 * (blockIdx.x - NRED) + (t >> 5), part = t & 31, nrows = mb / R;
@@ -748,8 +778,10 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     const int64_t il = mine ? i0 : 0;
     const uint2 gv = *(const uint2 *)(g + il);
     float4 pv = *(const float4 *)(a.p + il), mv = *(const float4 *)(a.m + il), vv = *(const float4 *)(a.v + il);
-    float acc = 0.f;
-    for (int j = threadIdx.x; j < NRED + NBIASB; j += blockDim.x) acc += w.npart[j];
+    static_assert(NRED + NBIASB > 512 && NRED + NBIASB <= 768, "three norm partials per lane");
+    const int j = threadIdx.x;   // blockDim.x == 256; the three loads are in flight together
+    const float n0 = w.npart[j], n1 = w.npart[j + 256], n2 = j + 512 < NRED + NBIASB ? w.npart[j + 512] : 0.f;
+    const float acc = ((0.f + n0) + n1) + n2;
     const float norm = sqrtf(block_sum(acc, red));
     if (!(norm <= 3.4028235e38f) || a.step[2] != 0.f) {   // NaN fails the comparison
         if (blockIdx.x == 0 && threadIdx.x == 0) {
