@@ -164,13 +164,13 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
     wload(wb[0], 0);
     wload(wb[1], 1);
     wload(wb[2], 2);
+    // the sample rows: their observation offsets go to LDS first, so that the row loads below
+    // wait for one load level only; the per-sample scalars are loaded after the rows and
+    // reach LDS at the barrier halfway through layer 1 (the loss reads them much later)
+    int64_t srow = 0;
     if (t < R) {
-        const int64_t s = clamp_index(a.perm[base + t], a.n);   // entries outside [0, n) are a caller error
-        soff[t] = s * K1;
-        sact[t] = (int)a.actions[s];
-        sold[t] = a.logp_old[s];
-        sadv[t] = a.adv[s];
-        sret[t] = a.ret[s];
+        srow = clamp_index(a.perm[base + t], a.n);   // entries outside [0, n) are a caller error
+        soff[t] = srow * K1;
     }
     __syncthreads();
     // The 32 observation rows, in units of 16 rows x 4 inputs: widened to bf16 into the LDS
@@ -186,6 +186,14 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
     for (int j = 0; j < 16; j++) xa[j] = *(const uint32_t *)(a.obs + soff[16 * pa + j] + 4 * ka);   // unconditional:
 #pragma unroll
     for (int j = 0; j < 16; j++) xb[j] = *(const uint32_t *)(a.obs + soff[16 * pbb + j] + 4 * kb);  // spare lanes repeat
+    int sa = 0;
+    float so = 0.f, sd = 0.f, sr = 0.f;
+    if (t < R) {
+        sa = (int)a.actions[srow];
+        so = a.logp_old[srow];
+        sd = a.adv[srow];
+        sr = a.ret[srow];
+    }
     auto xstore = [&](const uint32_t (&x)[16], int p, int kg) {
 #pragma unroll
         for (int j = 0; j < 16; j++) *(uint2 *)(xs + (16 * p + j) * XR + 4 * kg) = widen4(x[j]);
@@ -224,8 +232,9 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int ch = i0 + u;
-                if (ch == 14) {   // the second half of the x rows (uniform branch)
+                if (ch == 14) {   // the second half of the x rows and the sample scalars (uniform branch)
                     if (t < 2 * KBN) xstore(xb, pbb, kb);
+                    if (t < R) sact[t] = sa, sold[t] = so, sadv[t] = sd, sret[t] = sr;
                     __syncthreads();
                 }
                 if (ch + 3 < C1) wload(wb[(u + 3) & 3], ch + 3);
