@@ -62,13 +62,14 @@ def test_hip_matches_oracle(pkg, name, spec, batch, steps, nact):
     print(f'[parity] {name} ok, {dones} episode ends', flush=True)
 
 
-@pytest.mark.parametrize('spec', [('baseline_config', 8), ('reference_config', 8), ('v1_config', 8)])
+@pytest.mark.parametrize('spec', [('baseline_config', 8), ('reference_config', 8), ('v1_config', 8),
+                                  ('reference_config', 24), ('stress_config',)])
 def test_step_without_hash_is_the_same_step(pkg, spec):
     """Env(hash=False) passes no hash buffer and the digest is skipped. Every step's state
     rows, observation and out[] must equal those of the same worlds stepped with the digest
     (the path test_hip_matches_oracle checks against the oracle every step), over moves,
-    REST, descents and episode ends, on generated levels and on map 1057; the hash tensor
-    keeps its value."""
+    REST, descents and episode ends, on generated levels and on map 1057, in the <= 8
+    monster and the crowded builds; the hash tensor keeps its value."""
     print(f'[parity] hash off {spec}', flush=True)
     cfg = make(pkg, spec)
     n = 2048
