@@ -305,3 +305,45 @@ def test_v1_free_move_kill_deadline_and_death():
     w.f['hp'], w.f['regen'] = -100, 0
     out = w.transition(c, WAIT)
     assert out[6] == 1 and out[4] == 0 and w.f['hp'] == c.hp
+
+
+# ---------------------------------------------------------------- gpu-d1/scripts/test_learning.py:19-36,40-60
+def v1_invariants(f, floor, c):
+    """gpu-d1/scripts/test_learning.py:19-36 on every world of a batch."""
+    for j in range(len(f)):
+        s = f[j]
+        live = [i for i in range(c.count) if s['mhp'][i] > 0]
+        occ = s['occ']
+        assert s['killed'] == c.count - len(live), j
+        assert 0 < s['hp'] <= c.hp and 0 <= s['regen'] < 100 and 0 <= s['ticks'] < c.limit, j
+        assert floor[s['player']] and occ[s['player']] == -1, j
+        assert np.count_nonzero(occ >= 0) == len(live), j
+        assert len({int(s['pos'][i]) for i in live}) == len(live), j
+        for i in range(c.count):
+            if i in live:
+                p = int(s['pos'][i])
+                assert floor[p] and occ[p] == i and s['energy'][i] < 80, (j, i)
+            else:
+                assert s['energy'][i] == -30000, (j, i)
+
+
+@pytest.mark.parametrize('count', [1, 6, 8])
+def test_v1_state_invariants_every_step(count):
+    """The reference's learning test checks every world after the reset and between steps:
+    the kill count equals the monsters no longer alive, 0 < HP <= 18, 0 <= regen < 100,
+    0 <= ticks < 256, the player stands on a floor cell no monster occupies, there is one
+    occupancy entry per living monster, at a distinct floor cell, holding its index, living
+    monsters hold energy < 80 (every one that reached 80 has acted) and dead ones -30000.
+    37 worlds, seed 91 and 1/6/8 enemies as there, controller and random decisions
+    alternating over episode ends and resets; the invariants cover the reset's placement."""
+    c = pkg.config.v1_config(count)
+    env = O.OracleEnv(37, c, seed=91, threads=2)
+    rng = np.random.default_rng(137)
+    ends = 0
+    for k in range(600):
+        v1_invariants(env.fields(), env.floor, c)
+        a = env.heuristic() if k % 2 == 0 else rng.integers(0, 19, 37).astype(np.int64)
+        env.step(a)
+        ends += int(env.out[:, 1].sum())
+    v1_invariants(env.fields(), env.floor, c)
+    assert ends > 0
