@@ -646,6 +646,33 @@ __device__ __forceinline__ void primitive_learn(LCtx &c, int d, int limit, POut 
     if (o.done) { x.episode++; reset_learn<CLUMP>(c); }
 }
 
+// The later turns of a REST whose first turn left no living monster awake. Each repeats that
+// turn (learn.cu:684-828 with a WAIT) except for HP, regeneration and ticks: the player and
+// every monster stand still, so no monster can wake (detection depends on positions only)
+// and none acts, the view, memory, frontier list and sightings are already current, and no
+// random number is drawn. The loop keeps what changes, in the order the turn and the REST
+// loop change it. It returns true once HP is full (the REST ends), false before the turn
+// that reaches the deadline, which the caller runs as a whole turn (it ends the episode
+// and resets the world).
+__device__ __forceinline__ bool rest_quiet(LCtx &c, int limit, POut &o, int &elapsed, float &total, float &discounted,
+                                           float &factor) {
+    Ctx &x = c.x;
+    const D1Config *cf = x.c;
+    while (x.ticks + 1 < limit) {
+        x.regen += cf->regen;
+        while (x.regen >= 100) { x.hp = imin(cf->hp, x.hp + 1); x.regen -= 100; }
+        x.ticks++;
+        elapsed++;
+        total += o.reward;
+        discounted += factor * o.reward;
+        factor *= 1.f;
+        o.hp = imax(0, x.hp);
+        o.ticks = x.ticks;
+        if (x.hp >= cf->hp) return true;
+    }
+    return false;
+}
+
 // Joint action (learn.cu:853-875): MOVE 0-7, ATTACK 8-15, WAIT 16, REST 17, DESCEND 18.
 template <int CLUMP>
 __device__ __forceinline__ void transition_learn(LCtx &c, int action, int limit, float *out) {
@@ -673,6 +700,7 @@ __device__ __forceinline__ void transition_learn(LCtx &c, int action, int limit,
         if (o.done || invalid || action != 17) break;
         interrupted = o.saw_awake;
         if (interrupted || x.hp >= cf->hp) break;
+        if (!ballot(lane_alive(c) && x.mawake) && rest_quiet(c, limit, o, elapsed, total, discounted, factor)) break;
     }
     if (!o.done) x.decisions = decisions;
     if (!out) return;

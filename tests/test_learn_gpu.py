@@ -52,12 +52,13 @@ def compare_state(L, O, gpu_env, ref, step):
             f'frontier list env {i} step {step}'
 
 
-def run_parity(L, O, floors, batch, steps, seed, clump, map_filter, check_state_every=1):
+def run_parity(L, O, floors, batch, steps, seed, clump, map_filter, check_state_every=1, limit=2048, rest_every=0):
     maps = L.LearnMaps(np.stack(floors))
     host = O.LearnTablesHost(np.stack(floors))
     assert np.array_equal(maps.los.cpu().numpy().view(np.uint32), host.los), 'LOS tables differ'
-    env = L.LearnEnv(batch, seed=seed, maps=maps, map_filter=map_filter, clump=clump)
-    ref = O.OracleLearn(batch, host, seed=seed, clump=clump, map_filter=map_filter, threads=8)
+    env = L.LearnEnv(batch, seed=seed, maps=maps, map_filter=map_filter, clump=clump, limit=limit)
+    ref = O.OracleLearn(batch, host, seed=seed, clump=clump, map_filter=map_filter, limit=limit, threads=8)
+    ref.deadline_rests = 0
     rng = np.random.default_rng(seed)
     torch.cuda.synchronize()
     for step in range(steps):
@@ -68,13 +69,17 @@ def run_parity(L, O, floors, batch, steps, seed, clump, map_filter, check_state_
             compare_state(L, O, env, ref, step)
         h = ref.heuristic()
         assert np.array_equal(env.heuristic().cpu().numpy(), h), f'heuristic at step {step}'
-        if step % 3 == 2:   # mix in random (also invalid) actions
+        if rest_every and step % rest_every == 0:
+            a = np.full(batch, 17, np.int64)
+        elif step % 3 == 2:   # mix in random (also invalid) actions
             a = rng.integers(-1, 21, batch).astype(np.int64)
         else:
             a = h
         env.step(torch.from_numpy(a).cuda())
         assert ref.step(a) == 0
         assert np.array_equal(env.out.cpu().numpy().view(np.uint32), ref.out.view(np.uint32)), f'out at step {step}'
+        o = ref.out   # REST decisions of several turns that ran into the deadline
+        ref.deadline_rests += int(((o[:, 34] > 0) & (o[:, 35] > 1) & (o[:, 7] > 0)).sum())
     compare_state(L, O, env, ref, steps)
     return env, ref
 
@@ -96,6 +101,16 @@ def test_parity_multimap_clumped(L, O):
     env, ref = run_parity(L, O, floors, batch=48, steps=240, seed=5, clump=1, map_filter=-2, check_state_every=4)
     assert len(set(ref.scalar('map_id').tolist())) > 1
     assert ref.scalar('placement_clumped').any()
+
+
+def test_parity_rests_into_the_deadline(L, O):
+    """60-turn episodes with a REST decision every other step: many-turn rests end at full
+    HP or run into the deadline (the turn that reaches it ends the episode and resets the
+    world), on top of the controller's and random decisions; every step equals the CPU
+    restatement's, observation, mask, outcome row and state."""
+    env, ref = run_parity(L, O, [O.pkg.data.map1057()['floor']], batch=96, steps=300, seed=7, clump=0, map_filter=-1,
+                          check_state_every=2, limit=60, rest_every=2)
+    assert ref.deadline_rests > 20, ref.deadline_rests
 
 
 def test_active_mask_freezes_worlds(L, O):
