@@ -132,3 +132,18 @@ def test_policy_fwd_validation_without_gpu(pkg):
     assert L.d1_policy_fwd(fake + 4, 4, fake, fake, fake, fake, fake, fake, None) == -1   # obs not 8-byte aligned
     assert L.d1_policy_fwd(fake, 4, fake + 8, fake, fake, fake, fake, fake, None) == -1   # packed weights not 16-byte aligned
     assert L.d1_policy_fwd(fake, 4, fake, fake, fake, fake, fake + 4, fake, None) == -1   # logits not 16-byte aligned
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    """No CPU fallback: with the HIP library absent, loading it (what every entry point does
+    first) raises and names the build step."""
+    import importlib
+    L = importlib.import_module('dcss-auto_amd._lib')
+    monkeypatch.setattr(L, '_LIB', None)
+    monkeypatch.setattr(L, 'LIB_PATH', tmp_path / 'libd1hip.so')
+    with pytest.raises(RuntimeError, match='no CPU fallback'):
+        L.load()
+    monkeypatch.setattr(L, '_LEARN', {})
+    monkeypatch.setattr(L, 'HERE', tmp_path)
+    with pytest.raises(RuntimeError, match='no CPU fallback'):
+        L.load_learn(1)
