@@ -675,7 +675,8 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
         qlag = plag - 1;
         return best;
     }
-    if (!x.c->repair) return -1;
+    // With no walkable neighbour the search would queue nothing after p and find nothing.
+    if (!x.c->repair || !ballot(c.walk)) return -1;
     const int fd = repair_search(x, px, py, plx, ply, mp, imin(plag, RQ_FAR - 1));
     if (fd < 0) return -1;
     const int sx = px + ddx(fd), sy = py + ddy(fd);
