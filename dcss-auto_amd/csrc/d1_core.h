@@ -56,6 +56,13 @@ template <int CTRL, int ROWS = 0xF>
 __device__ __forceinline__ int dpp(int v, int id) { return __builtin_amdgcn_update_dpp(id, v, CTRL, ROWS, 0xF, false); }
 constexpr int DPP_QUAD_1032 = 0xB1, DPP_QUAD_2301 = 0x4E, DPP_ROW_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140,
               DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143, DPP_WAVE_SHL1 = 0x130, DPP_WAVE_SHR1 = 0x138;
+// lane l <- l-1 / l+1; bound control makes lane 0 / lane 63 (no source lane) read 0
+__device__ __forceinline__ uint32_t lane_up(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_WAVE_SHR1, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint32_t lane_dn(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_WAVE_SHL1, 0xF, 0xF, true);
+}
 // Whole-wave reductions (every lane active): pairs, quads, half rows and rows by lane
 // permutations, then row 0 into row 1 and row 2 into row 3 (row_bcast:15), rows 0-1 into
 // rows 2-3 (row_bcast:31); lane 63 ends with the wave's result.
@@ -647,6 +654,72 @@ __device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, in
     __syncthreads();
     return result;
 }
+// A sufficient test that the detour search finds nothing, without its queue. The search
+// queues cells in breadth-first order from p over walkable cells, so the cells it queues
+// lie within the first D rings around p, where D is the first ring that brings the count
+// (p included) to REPAIR_Q, or the component's last ring. It succeeds only at a queued
+// cell of layer plag with a walkable neighbour of layer plag - 1 (queued cells are never
+// lower than p and neighbours differ by at most one layer), and that neighbour lies within
+// ring D + 1. The rings are grown here as bitmaps of a 32 x 64 window (lane = row py-31+l,
+// bit = column px-15+b), and every ringed cell carries the set of layer offsets from plag it
+// may have: {0}, {1}, {2} or ">= 3", derived from its layer mod 3 and the sets of its
+// neighbours in earlier rings (a reached neighbour is one layer away at most; an unreached
+// cell lies past the field's last layer). Until a cell can be lower than p these sets
+// contain the true offsets, so a cell of layer mod 3 == plag - 1 next to a possible offset 0
+// is the first place where a lower cell can appear. Returns true when rings 1..D+1 hold no
+// such cell; false (run the search) when one may exist or the rings reach the window edge.
+__device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, int plx, int ply, int mp) {
+    const Smem *sm = x.sm;
+    const int y = py - 31 + x.lane;
+    // window bit b is column px-15+b; with a zero word prepended to the row, that is bit
+    // vb+b of the widened row, vb = px+17 in 17..96: words j = vb/32 and j+1, shifted by vb%32
+    const int vb = px + 17, j = vb >> 5, s = vb & 31;
+    uint32_t fl = 0, oc = 0, re = 0, l0 = 0, l1 = 0;
+    if ((unsigned)y < (unsigned)H) {
+        // widened words j and j+1 are row words j-1 and j when those exist (j-1 >= 0, j <= 2);
+        // the indices are clamped into the row so that every address read is in range
+        const bool lo_in = j >= 1, hi_in = j <= RW - 1;
+        const int wl = y * RW + imax(j - 1, 0), wh = y * RW + imin(j, RW - 1);
+        auto win = [&](const uint32_t *bm) {
+            const uint32_t lo = bm[wl], hw = bm[wh];
+            return __builtin_amdgcn_alignbit(hi_in ? hw : 0u, lo_in ? lo : 0u, s);
+        };
+        fl = win(sm->floor);
+        oc = win(sm->occ);
+        re = win(sm->reach);
+        l0 = win(sm->lay0);
+        l1 = win(sm->lay1);
+    }
+    uint32_t walk = fl & ~oc;
+    const int pb = plx - px + 15;
+    if (x.lane == ply - py + 31 && (unsigned)pb < 32u) walk &= ~(1u << pb);
+    // cells by layer offset class from p: layer mod 3 == mp, mp + 1, mp + 2 (reached cells)
+    const uint32_t z = re & ~(l0 | l1);
+    const uint32_t c0 = mp == 0 ? z : mp == 1 ? l0 : l1;
+    const uint32_t c1 = mp == 0 ? l0 : mp == 1 ? l1 : z;
+    const uint32_t c2 = mp == 0 ? l1 : mp == 1 ? z : l0;
+    auto dil = [](uint32_t v) {
+        const uint32_t h = v | (v << 1) | (v >> 1);
+        return h | lane_up(h) | lane_dn(h);
+    };
+    uint32_t p0 = x.lane == 31 ? 1u << 15 : 0u, p1 = 0, p2 = 0, hi = 0, seen = p0;
+    int count = 1, stop = -1;
+    for (int k = 1;; k++) {
+        const uint32_t d0 = dil(p0), d1 = dil(p1), d2 = dil(p2), dh = dil(hi);
+        const uint32_t n = (d0 | d1 | d2 | dh) & walk & ~seen;
+        if (ballot((n & c2 & d0) != 0)) return false;   // possibly lower than p
+        if (!ballot(n != 0)) return true;               // the component ends
+        p0 |= n & c0 & (d0 | d1);
+        p1 |= n & c1 & (d0 | d1 | d2);
+        p2 |= n & c2 & (d1 | d2 | dh);
+        hi |= (n & c0 & (d2 | dh)) | (n & (c1 | c2) & dh) | (n & ~re);
+        seen |= n;
+        count += (int)wave_sum((uint32_t)__popc(n));
+        if (k == stop) return true;
+        if (ballot((n & 0x80000001u) != 0 || ((x.lane == 0 || x.lane == 63) && n != 0))) return false;
+        if (stop < 0 && count >= REPAIR_Q) stop = k + 1;
+    }
+}
 // gpu-d1/src/sim.h:207-253: greedy descent with rotated order and 1/ties
 // replacement, then a bounded 24-node BFS detour when stuck. p is a reached cell at
 // absolute layer plag (every mover is reached before the field stops growing); the chosen
@@ -676,7 +749,7 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
         return best;
     }
     // With no walkable neighbour the search would queue nothing after p and find nothing.
-    if (!x.c->repair || !ballot(c.walk)) return -1;
+    if (!x.c->repair || !ballot(c.walk) || detour_ruled_out(x, px, py, plx, ply, mp)) return -1;
     const int fd = repair_search(x, px, py, plx, ply, mp, imin(plag, RQ_FAR - 1));
     if (fd < 0) return -1;
     const int sx = px + ddx(fd), sy = py + ddy(fd);
@@ -690,13 +763,6 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
 // planes in registers; vertical neighbours arrive by DPP lane shifts, so a layer has no LDS
 // access and no barrier. Reach and the planes are published to LDS at the end (the monster
 // phase reads them); the frontier bitmap is left clear for the repair search's marks.
-// lane l <- l-1 / l+1; bound control makes lane 0 / lane 63 (no source lane) read 0
-__device__ __forceinline__ uint32_t lane_up(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_WAVE_SHR1, 0xF, 0xF, true);
-}
-__device__ __forceinline__ uint32_t lane_dn(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_WAVE_SHL1, 0xF, 0xF, true);
-}
 __device__ __forceinline__ Row row_up(Row r) { return {lane_up(r.a), lane_up(r.b), lane_up(r.c)}; }
 __device__ __forceinline__ Row row_dn(Row r) { return {lane_dn(r.a), lane_dn(r.b), lane_dn(r.c)}; }
 __device__ __forceinline__ Row row_lane(Row r, int l) {
