@@ -661,13 +661,15 @@ __device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, in
 // cell of layer plag with a walkable neighbour of layer plag - 1 (queued cells are never
 // lower than p and neighbours differ by at most one layer), and that neighbour lies within
 // ring D + 1. The rings are grown here as bitmaps of a 32 x 64 window (lane = row py-31+l,
-// bit = column px-15+b), and every ringed cell carries the set of layer offsets from plag it
-// may have: {0}, {1}, {2} or ">= 3", derived from its layer mod 3 and the sets of its
+// bit = column px-15+b), and every ringed cell is put in the classes of layer offset from
+// plag it may have: 0, 1 or ">= 2" (p0, p1, g), from its layer mod 3 and the classes of its
 // neighbours in earlier rings (a reached neighbour is one layer away at most; an unreached
-// cell lies past the field's last layer). Until a cell can be lower than p these sets
-// contain the true offsets, so a cell of layer mod 3 == plag - 1 next to a possible offset 0
-// is the first place where a lower cell can appear. Returns true when rings 1..D+1 hold no
-// such cell; false (run the search) when one may exist or the rings reach the window edge.
+// cell lies past the field's last layer): offset 0 needs a neighbour in 0 or 1, offset 1 any
+// neighbour, ">= 2" a neighbour in ">= 2" (or in 1, for layer mod 3 == plag + 2). Until a
+// cell can be lower than p the classes contain the true offsets, so a cell of layer mod 3 ==
+// plag - 1 next to a possible offset 0 is the first place where a lower cell can appear.
+// Returns true when rings 1..D+1 hold no such cell; false (run the search) when one may
+// exist or the rings reach the window edge.
 __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, int plx, int ply, int mp) {
     const Smem *sm = x.sm;
     const int y = py - 31 + x.lane;
@@ -702,17 +704,16 @@ __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, i
         const uint32_t h = v | (v << 1) | (v >> 1);
         return h | lane_up(h) | lane_dn(h);
     };
-    uint32_t p0 = x.lane == 31 ? 1u << 15 : 0u, p1 = 0, p2 = 0, hi = 0, seen = p0;
+    uint32_t p0 = x.lane == 31 ? 1u << 15 : 0u, p1 = 0, g = 0, seen = p0;
     int count = 1, stop = -1;
     for (int k = 1;; k++) {
-        const uint32_t d0 = dil(p0), d1 = dil(p1), d2 = dil(p2), dh = dil(hi);
-        const uint32_t n = (d0 | d1 | d2 | dh) & walk & ~seen;
+        const uint32_t d0 = dil(p0), d1 = dil(p1), dg = dil(g);
+        const uint32_t n = (d0 | d1 | dg) & walk & ~seen;
         if (ballot((n & c2 & d0) != 0)) return false;   // possibly lower than p
         if (!ballot(n != 0)) return true;               // the component ends
         p0 |= n & c0 & (d0 | d1);
-        p1 |= n & c1 & (d0 | d1 | d2);
-        p2 |= n & c2 & (d1 | d2 | dh);
-        hi |= (n & c0 & (d2 | dh)) | (n & (c1 | c2) & dh) | (n & ~re);
+        p1 |= n & c1;   // every new cell neighbours an earlier one
+        g |= n & (dg | (c2 & d1) | ~re);
         seen |= n;
         count += (int)wave_sum((uint32_t)__popc(n));
         if (k == stop) return true;
