@@ -705,20 +705,22 @@ __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, i
         return h | lane_up(h) | lane_dn(h);
     };
     uint32_t p0 = x.lane == 31 ? 1u << 15 : 0u, p1 = 0, g = 0, seen = p0;
-    int count = 1, stop = -1;
-    for (int k = 1;; k++) {
+    int count = 1;
+    for (bool last = false;; ) {
         const uint32_t d0 = dil(p0), d1 = dil(p1), dg = dil(g);
         const uint32_t n = (d0 | d1 | dg) & walk & ~seen;
         if (ballot((n & c2 & d0) != 0)) return false;   // possibly lower than p
-        if (!ballot(n != 0)) return true;               // the component ends
+        const uint64_t rows = ballot(n != 0);
+        if (!rows) return true;                         // the component ends
+        if (last) return true;                          // ring D + 1 done
+        // the next ring would leave the window: new cells in its first or last row or column
+        if ((rows & 0x8000000000000001ull) || ballot((n & 0x80000001u) != 0)) return false;
         p0 |= n & c0 & (d0 | d1);
         p1 |= n & c1;   // every new cell neighbours an earlier one
         g |= n & (dg | (c2 & d1) | ~re);
         seen |= n;
         count += (int)wave_sum((uint32_t)__popc(n));
-        if (k == stop) return true;
-        if (ballot((n & 0x80000001u) != 0 || ((x.lane == 0 || x.lane == 63) && n != 0))) return false;
-        if (stop < 0 && count >= REPAIR_Q) stop = k + 1;
+        last = count >= REPAIR_Q;                       // this was ring D
     }
 }
 // gpu-d1/src/sim.h:207-253: greedy descent with rotated order and 1/ties
