@@ -664,8 +664,11 @@ __device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, in
 // bit = column px-15+b), and every ringed cell is put in the classes of layer offset from
 // plag it may have: 0, 1 or ">= 2" (p0, p1, g), from its layer mod 3 and the classes of its
 // neighbours in earlier rings (a reached neighbour is one layer away at most; an unreached
-// cell that p can walk to lies past the field's last layer, which every field builds at least
-// two layers past every mover, so its offset is >= 3): offset 0 needs a neighbour in 0 or 1, offset 1 any
+// cell that p can walk to lies past the field's last layer, which is built ceil(speed/10)
+// >= 2 layers past every mover's starting layer while a mover acts at most ceil(speed/10)
+// times a turn and climbs at most one layer per act, so p is at least one layer below the
+// last and that cell's offset is >= 2; the static and exhaustive fields reach every cell p
+// can walk to): offset 0 needs a neighbour in 0 or 1, offset 1 any
 // neighbour, ">= 2" a neighbour in ">= 2" (or in 1, for layer mod 3 == plag + 2). Until a
 // cell can be lower than p the classes contain the true offsets, so a cell of layer mod 3 ==
 // plag - 1 next to a possible offset 0 is the first place where a lower cell can appear.
