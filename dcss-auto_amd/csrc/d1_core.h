@@ -39,7 +39,11 @@ struct Smem {
         };
         float stage[D1_STAGE_FLOATS];
     };
-    uint32_t rq[32];   // the repair search's queue (packed entries)
+    uint32_t rq[24];   // the repair search's queue (packed entries)
+    // the player view when a kernel keeps it in LDS (Ctx::view_lds), quadrant q in words 2q
+    // (low) and 2q+1; 32-bit words keep the struct's alignment at 4 bytes, so that kernels
+    // that embed it do not grow (a one-wave workgroup at 10,240 B fits 16 to a CU)
+    uint32_t vis[8];
 };
 
 // ---------------------------------------------------------------- small helpers
@@ -316,7 +320,11 @@ struct Ctx {
     int player, hp, regen, blocks, ticks, killed, decisions, floor_seen, episode, first_stair_tick, ncells;
     uint64_t stairs;   // three int16 cells at bits 0, 16, 32 (-1 = none)
     uint32_t t, env_id;
-    uint64_t vis0, vis1, vis2, vis3;   // player view, quadrants (+,+) (-,+) (-,-) (+,-)
+    // player view, quadrants (+,+) (-,+) (-,-) (+,-): bit 8*|dy| + |dx|. Kept in wave-uniform
+    // registers, or in Smem::vis where a kernel sets view_lds (a constant per kernel): the
+    // crowded step's monster phase holds enough live values that the registers spill.
+    uint64_t visr[4];
+    bool view_lds = false;
     // this lane's monster (lane < count)
     int mpos, mhp, menergy, mawake, mkind;
     int mlay;    // absolute BFS layer of the monster's cell (FAR when not known)
@@ -331,6 +339,21 @@ struct Ctx {
     int vlo = 0, vhi = H - 1;
 };
 
+// the four quadrant view masks (wave-uniform)
+__device__ __forceinline__ void set_view(Ctx &x, uint64_t v0, uint64_t v1, uint64_t v2, uint64_t v3) {
+    if (x.view_lds) {
+        if (x.lane < 8) {
+            const uint64_t v = x.lane < 2 ? v0 : x.lane < 4 ? v1 : x.lane < 6 ? v2 : v3;
+            x.sm->vis[x.lane] = (uint32_t)(x.lane & 1 ? v >> 32 : v);
+        }
+        __syncthreads();
+    } else {
+        x.visr[0] = v0; x.visr[1] = v1; x.visr[2] = v2; x.visr[3] = v3;
+    }
+}
+__device__ __forceinline__ uint64_t view_q(const Ctx &x, int q) {
+    return x.view_lds ? (uint64_t)x.sm->vis[2 * q + 1] << 32 | x.sm->vis[2 * q] : x.visr[q];
+}
 __device__ __forceinline__ int stair_at(const Ctx &x, int k) { return (int16_t)(uint16_t)(x.stairs >> (16 * k)); }
 __device__ __forceinline__ uint64_t pack_stairs(int a, int b, int c) {
     return (uint64_t)(uint16_t)a | (uint64_t)(uint16_t)b << 16 | (uint64_t)(uint16_t)c << 32;
@@ -342,10 +365,10 @@ __device__ __forceinline__ bool vis_rel(const Ctx &x, int dx, int dy) {
     if (iabs(dx) > 7 || iabs(dy) > 7) return false;
     int b = iabs(dy) * 8 + iabs(dx);
     uint64_t v = 0;
-    if (dx >= 0 && dy >= 0) v |= x.vis0;
-    if (dx <= 0 && dy >= 0) v |= x.vis1;
-    if (dx <= 0 && dy <= 0) v |= x.vis2;
-    if (dx >= 0 && dy <= 0) v |= x.vis3;
+    if (dx >= 0 && dy >= 0) v |= view_q(x, 0);
+    if (dx <= 0 && dy >= 0) v |= view_q(x, 1);
+    if (dx <= 0 && dy <= 0) v |= view_q(x, 2);
+    if (dx >= 0 && dy <= 0) v |= view_q(x, 3);
     return (v >> b) & 1;
 }
 // in_view, gpu-d1/branches/d1-stairs-v2/src/learn.cu:192-198 (terrain LOS, radius 7)
@@ -388,10 +411,8 @@ __device__ __forceinline__ void compute_view(Ctx &x) {
 #undef D1_RAY_TEST
     }
     int tx = x.lane & 7, ty = x.lane >> 3;
-    x.vis0 = ballot(a0 && inb(px + tx, py + ty));
-    x.vis1 = ballot(a1 && inb(px - tx, py + ty));
-    x.vis2 = ballot(a2 && inb(px - tx, py - ty));
-    x.vis3 = ballot(a3 && inb(px + tx, py - ty));
+    set_view(x, ballot(a0 && inb(px + tx, py + ty)), ballot(a1 && inb(px - tx, py + ty)),
+             ballot(a2 && inb(px - tx, py - ty)), ballot(a3 && inb(px + tx, py - ty)));
 }
 // LOS from a monster to the player within Chebyshev 6 (monster_detects_player,
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:199-207).
@@ -425,8 +446,8 @@ __device__ __forceinline__ int reveal(Ctx &x) {
     if (mine) {
         int ay = iabs(dy);
         uint32_t R = 0, L = 0;
-        if (dy >= 0) { R |= (uint32_t)(x.vis0 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis1 >> (8 * ay)) & 0xFFu; }
-        if (dy <= 0) { R |= (uint32_t)(x.vis3 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis2 >> (8 * ay)) & 0xFFu; }
+        if (dy >= 0) { R |= (uint32_t)(view_q(x, 0) >> (8 * ay)) & 0xFFu; L |= (uint32_t)(view_q(x, 1) >> (8 * ay)) & 0xFFu; }
+        if (dy <= 0) { R |= (uint32_t)(view_q(x, 3) >> (8 * ay)) & 0xFFu; L |= (uint32_t)(view_q(x, 2) >> (8 * ay)) & 0xFFu; }
         uint32_t v15 = (__builtin_bitreverse32(L) >> 24) | (R << 7);
         mask = row_place15(v15, px);
         Row old = row_ld(x.sm->viewed, y);
@@ -584,6 +605,7 @@ __device__ __forceinline__ Cell cell_at(const Smem *sm, int x, int y, int plx, i
 // an unreached cell is on the field's last layer; an unreached cell lies beyond every layer
 // that could be lower than p.
 constexpr int REPAIR_Q = 24, RQ_FAR = 8191;
+static_assert(REPAIR_Q <= (int)(sizeof(Smem::rq) / sizeof(uint32_t)), "the queue fits Smem::rq");
 __device__ __forceinline__ uint32_t rq_pack(int x, int y, int fdir, int m3, int lay) {
     return (uint32_t)x | (uint32_t)y << 7 | (uint32_t)fdir << 14 | (uint32_t)m3 << 17 | (uint32_t)imin(lay, RQ_FAR) << 19;
 }

@@ -302,8 +302,8 @@ __device__ __forceinline__ void write_obs(Ctx &x, uint8_t *o) {
             const uint32_t fr = row_strip15(row_and(row_and(fl, vw), u), px) & ib;
             const int ay = iabs(dy);
             uint32_t R = 0, L = 0;
-            if (dy >= 0) { R |= (uint32_t)(x.vis0 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis1 >> (8 * ay)) & 0xFFu; }
-            if (dy <= 0) { R |= (uint32_t)(x.vis3 >> (8 * ay)) & 0xFFu; L |= (uint32_t)(x.vis2 >> (8 * ay)) & 0xFFu; }
+            if (dy >= 0) { R |= (uint32_t)(view_q(x, 0) >> (8 * ay)) & 0xFFu; L |= (uint32_t)(view_q(x, 1) >> (8 * ay)) & 0xFFu; }
+            if (dy <= 0) { R |= (uint32_t)(view_q(x, 3) >> (8 * ay)) & 0xFFu; L |= (uint32_t)(view_q(x, 2) >> (8 * ay)) & 0xFFu; }
             const uint32_t vis = ((__builtin_bitreverse32(L) >> 24) | (R << 7)) & ib;
             w0 = ((~ib | (v & ~f)) & 0x7FFFu) | ((v & f & ib) << 16);
             w1 = vis | (fr << 16);
@@ -392,7 +392,7 @@ __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
         ((Mon *)(row + OFF_MON))[x.lane] = m;
     }
     if (x.lane < 4) {
-        uint64_t v = x.lane == 0 ? x.vis0 : x.lane == 1 ? x.vis1 : x.lane == 2 ? x.vis2 : x.vis3;
+        const uint64_t v = x.lane == 0 ? view_q(x, 0) : x.lane == 1 ? view_q(x, 1) : x.lane == 2 ? view_q(x, 2) : view_q(x, 3);
         ((uint64_t *)(row + OFF_VIEW))[x.lane] = v;
     }
     // the viewed rows this step changed: the reveal bands of the cells the player moved to,
@@ -495,8 +495,8 @@ __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
     const uint64_t rs = (uint64_t)hw(1) << 32 | hw(0), ri = (uint64_t)hw(3) << 32 | hw(2);
     if (RM == 0) x.g.pcg_load(rs, ri);
     else x.g.counter(rs, x.env_id, x.t, 0);
-    x.vis0 = (uint64_t)hw(17) << 32 | hw(16); x.vis1 = (uint64_t)hw(19) << 32 | hw(18);
-    x.vis2 = (uint64_t)hw(21) << 32 | hw(20); x.vis3 = (uint64_t)hw(23) << 32 | hw(22);
+    set_view(x, (uint64_t)hw(17) << 32 | hw(16), (uint64_t)hw(19) << 32 | hw(18), (uint64_t)hw(21) << 32 | hw(20),
+             (uint64_t)hw(23) << 32 | hw(22));
     if (x.lane < max_m) {
         x.mpos = (int16_t)(pf.mon.x & 0xFFFFu); x.mhp = (int16_t)(pf.mon.x >> 16);
         x.menergy = (int16_t)(pf.mon.y & 0xFFFFu); x.mawake = (pf.mon.y >> 16) & 0xFFu; x.mkind = pf.mon.y >> 24;
@@ -588,6 +588,7 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
     const int first = blk < g ? WPB * blk : WPB * g + (blk - g), last = imin(n, blk < g ? first + WPB : first + 1);
     Ctx x;
     x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
+    x.view_lds = WPB == CROWD_WPB;   // the crowded build keeps the player view in LDS
     Pre pf;
     prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
     for (int env = first; env < last; env++) {
@@ -759,7 +760,8 @@ __device__ __forceinline__ void wait_store(Ctx &x, uint8_t *row, int count, int 
 }
 __device__ __forceinline__ void wait_ctx(Ctx &x, Smem *sm, const D1Config *cfg, const D1WaitMap &map) {
     x.sm = sm; x.c = cfg; x.rays = nullptr; x.nslots = 0; x.lane = lane_id();
-    x.player = map.player; x.vis0 = x.vis1 = x.vis2 = x.vis3 = 0;
+    x.player = map.player;
+    set_view(x, 0, 0, 0, 0);
     x.mlay = FAR;
     x.lastl = 65535;   // the static field holds every reachable cell
 }

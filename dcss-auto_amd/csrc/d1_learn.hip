@@ -100,10 +100,8 @@ __device__ __forceinline__ void view_los(LCtx &c) {
     Ctx &x = c.x;
     const uint32_t *row = c.los + (size_t)x.player * 10;
     int px = x.player % W, py = x.player / W, tx = x.lane & 7, ty = x.lane >> 3;
-    x.vis0 = ballot(los_bit(row, tx, ty) && inb(px + tx, py + ty));
-    x.vis1 = ballot(los_bit(row, -tx, ty) && inb(px - tx, py + ty));
-    x.vis2 = ballot(los_bit(row, -tx, -ty) && inb(px - tx, py - ty));
-    x.vis3 = ballot(los_bit(row, tx, -ty) && inb(px + tx, py - ty));
+    set_view(x, ballot(los_bit(row, tx, ty) && inb(px + tx, py + ty)), ballot(los_bit(row, -tx, ty) && inb(px - tx, py + ty)),
+             ballot(los_bit(row, -tx, -ty) && inb(px - tx, py - ty)), ballot(los_bit(row, tx, -ty) && inb(px + tx, py - ty)));
 }
 // monster_detects_player (learn.cu:201-207) for this lane's monster
 __device__ __forceinline__ bool lane_detects(const LCtx &c, int origin) {
@@ -175,8 +173,8 @@ __device__ __forceinline__ int reveal_learn(LCtx &c) {
     if (mine) {
         int ay = iabs(dy);
         uint32_t R = 0, Lf = 0;
-        if (dy >= 0) { R |= (uint32_t)(x.vis0 >> (8 * ay)) & 0xFFu; Lf |= (uint32_t)(x.vis1 >> (8 * ay)) & 0xFFu; }
-        if (dy <= 0) { R |= (uint32_t)(x.vis3 >> (8 * ay)) & 0xFFu; Lf |= (uint32_t)(x.vis2 >> (8 * ay)) & 0xFFu; }
+        if (dy >= 0) { R |= (uint32_t)(view_q(x, 0) >> (8 * ay)) & 0xFFu; Lf |= (uint32_t)(view_q(x, 1) >> (8 * ay)) & 0xFFu; }
+        if (dy <= 0) { R |= (uint32_t)(view_q(x, 3) >> (8 * ay)) & 0xFFu; Lf |= (uint32_t)(view_q(x, 2) >> (8 * ay)) & 0xFFu; }
         uint32_t v15 = (__builtin_bitreverse32(Lf) >> 24) | (R << 7);
         mask = row_place15(v15, px);
         old = row_ld(sm->viewed, y);
@@ -966,7 +964,7 @@ __device__ __forceinline__ void setup(LCtx &c, LSmem *L, const D1Config *cfg, co
     c.L = L; c.t = t;
     c.x.sm = &L->s; c.x.c = cfg; c.x.rays = nullptr; c.x.nslots = 0; c.x.lane = lane_id();
     c.x.t = 0; c.x.env_id = 0; c.x.ncells = 0;
-    c.x.vis0 = c.x.vis1 = c.x.vis2 = c.x.vis3 = 0;
+    set_view(c.x, 0, 0, 0, 0);
     c.clumped = 0; c.error = 0;
 }
 
