@@ -832,11 +832,18 @@ __device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
     int m3 = 0, stop = 1 << 30, last = 0;
     for (int layer = 1; layer < N; layer++) {
         m3 = m3 == 2 ? 0 : m3 + 1;
-        const Row f1_0 = row_lane(f1, 0), f0_63 = row_lane(f0, 63);
-        const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, f1_0, row_dn(f0));
-        const Row u1 = row_sel(lane == 0, f0_63, row_up(f1)), d1 = row_sel(lane >= H - 65, zero, row_dn(f1));
-        const Row n0 = row_andn(row_and(dilate(f0, u0, d0), fl0), r0);
-        const Row n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), fl1), r1) : zero;
+        const Row f0_63 = row_lane(f0, 63);
+        Row n0, n1 = zero;
+        if (row_any(f0_63) || ballot(row_any(f1))) {   // rows 64.. can grow this layer
+            const Row f1_0 = row_lane(f1, 0);
+            const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, f1_0, row_dn(f0));
+            const Row u1 = row_sel(lane == 0, f0_63, row_up(f1)), d1 = row_sel(lane >= H - 65, zero, row_dn(f1));
+            n0 = row_andn(row_and(dilate(f0, u0, d0), fl0), r0);
+            n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), fl1), r1) : zero;
+        } else {   // no frontier in rows 63..: the second row set neither grows nor feeds row 63
+            const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, zero, row_dn(f0));
+            n0 = row_andn(row_and(dilate(f0, u0, d0), fl0), r0);
+        }
         if (!ballot(row_any(n0) || row_any(n1))) break;
         last = layer;
         r0 = row_or(r0, n0); r1 = row_or(r1, n1);
