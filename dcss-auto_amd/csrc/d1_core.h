@@ -757,8 +757,7 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
     int rotation = x.g.r(4);
     const Smem *sm = x.sm;
     const int px = p % W, py = p / W, plx = x.player % W, ply = x.player / W;
-    const Cell pc = cell_at(sm, px, py, plx, ply);
-    const int mp = pc.m3;
+    const int mp = plag < FAR ? plag % 3 : 0;   // p's layer mod 3, as its bit planes hold it
     const int z = x.lane & 7;
     const int d = z < 4 ? (z + rotation) & 3 : 4 + ((z + rotation) & 3);
     const int nx = px + ddx(d), ny = py + ddy(d);
