@@ -220,7 +220,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
             if (key < 0) break;
             int id = 127 - (key & 127);
             act(x, id);
-            if (in_view(x, lane_val(x.mpos, id))) saw = true;
+            if (!saw && in_view(x, lane_val(x.mpos, id))) saw = true;
         }
     }
     x.ticks++;
