@@ -615,7 +615,10 @@ __device__ __forceinline__ void primitive_learn(LCtx &c, int d, int limit, POut 
             if (key < 0) break;
             int id = 127 - (key & 127);
             act(x, id);
-            if (in_view(x, lane_val(x.mpos, id))) { o.saw_enemy = 1; if (lane_val(x.mawake, id)) o.saw_awake = 1; }
+            if (!(o.saw_enemy && o.saw_awake) && in_view(x, lane_val(x.mpos, id))) {   // nothing left to learn once both are set
+                o.saw_enemy = 1;
+                if (lane_val(x.mawake, id)) o.saw_awake = 1;
+            }
         }
     }
     x.ticks++;
