@@ -214,10 +214,9 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
             if (x.fcache) field_memo(x);
             else bfs(x, movers, imax(2, (maxspeed + 9) / 10));
         }
-        while (x.hp > 0) {
-            int key = (mine && x.menergy >= 80) ? x.menergy * 128 + 127 - x.lane : -1;
-            key = wave_max(key);
-            if (key < 0) break;
+        // a ballot ends the loop when no monster can act (most turns), before any reduction
+        while (x.hp > 0 && ballot(mine && x.menergy >= 80)) {
+            const int key = wave_max(mine && x.menergy >= 80 ? x.menergy * 128 + 127 - x.lane : -1);
             int id = 127 - (key & 127);
             act(x, id);
             if (!saw && in_view(x, lane_val(x.mpos, id))) saw = true;
