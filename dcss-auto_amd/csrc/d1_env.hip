@@ -162,7 +162,9 @@ __device__ __forceinline__ void field_memo(Ctx &x) {
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:684-827 with the v1 kill-all clear
 // (gpu-d1/src/learn.cu:549) as a switch. d: 0-7 move/bump, 8 wait, 18 descend.
 // Returns done; out8 = reward, done, clear, killed, hp, ticks, death, timeout.
-__device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw, const uint32_t *cells_g) {
+// `saw` (an awake monster was in view during the turn) is computed only when want_saw: REST
+// repeats read it, every other action ignores it.
+__device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw, bool want_saw, const uint32_t *cells_g) {
     const D1Config *c = x.c;
     Smem *sm = x.sm;
     int milli = c->step_milli;
@@ -193,7 +195,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
         }
     }
     if (moved) milli += c->explore_milli * reveal(x);   // an unmoved view reveals nothing new
-    saw = visible_awake(x);
+    saw = want_saw && visible_awake(x);
     bool clear = (d == 18 && stair_index(x) > 0 && x.hp > 0) || (c->clear_on_kill_all && x.killed == c->count);
     if (!clear) {
         bool mine = x.lane < c->count;
@@ -219,7 +221,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
             const int key = wave_max(mine && x.menergy >= 80 ? x.menergy * 128 + 127 - x.lane : -1);
             int id = 127 - (key & 127);
             act(x, id);
-            if (!saw && in_view(x, lane_val(x.mpos, id))) saw = true;
+            if (want_saw && !saw && in_view(x, lane_val(x.mpos, id))) saw = true;
         }
     }
     x.ticks++;
@@ -229,7 +231,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
     if (death) milli -= c->death_milli;
     float reward = 0.001f * (float)milli;
     reward -= c->turn_cost;
-    saw = saw || visible_awake(x);
+    saw = saw || (want_saw && visible_awake(x));
     bool done = clear || death || timeout;
     out8[0] = reward; out8[1] = done; out8[2] = clear; out8[3] = (float)x.killed;
     out8[4] = (float)imax(0, x.hp); out8[5] = (float)x.ticks; out8[6] = death; out8[7] = timeout;
@@ -254,7 +256,7 @@ __device__ __forceinline__ void transition(Ctx &x, int action, float *out, const
         else if (action == 18) { if (stair_index(x) > 0) d = 18; else invalid = true; }
         else if (action != 16) invalid = true;
         bool saw = false;
-        bool done = primitive(x, d, out8, saw, cells_g);
+        bool done = primitive(x, d, out8, saw, action == 17, cells_g);
         total += out8[0];
         if (done || invalid || action != 17) break;
         if (saw || x.hp >= c->hp) break;
