@@ -207,14 +207,16 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
             if (detects(x, pos) && x.lane == i) { x.mawake = 1; x.menergy = 70; }
         }
         if (mine && x.mhp > 0 && !x.mawake) x.menergy = -30000;
-        int maxspeed = 0;
         if (mine && x.mhp > 0) x.menergy += kind_speed(c, x.mkind);
-        for (int k = 0; k < 6; k++) maxspeed = imax(maxspeed, c->kinds[k].speed);
         x.menergy = (int16_t)x.menergy;
         uint64_t movers = ballot(mine && x.mhp > 0 && x.mawake && x.menergy >= 80 && cheb(x.mpos, x.player) > 1);
         if (movers) {
             if (x.fcache) field_memo(x);
-            else bfs(x, movers, imax(2, (maxspeed + 9) / 10));
+            else {
+                int maxspeed = 0;
+                for (int k = 0; k < 6; k++) maxspeed = imax(maxspeed, c->kinds[k].speed);
+                bfs(x, movers, imax(2, (maxspeed + 9) / 10));
+            }
         }
         // a ballot ends the loop when no monster can act (most turns), before any reduction
         while (x.hp > 0 && ballot(mine && x.menergy >= 80)) {
