@@ -723,10 +723,8 @@ __device__ __forceinline__ void wait_step(Ctx &x, const D1WaitMap &map, int coun
     while (x.regen >= 100) { x.hp = imin(x.c->hp, x.hp + 1); x.regen -= 100; }
     bool mine = x.lane < count;
     if (mine) x.menergy = (int16_t)(x.menergy + kind_speed(x.c, x.mkind));
-    while (x.hp > 0) {
-        int key = (mine && x.menergy >= 80) ? x.menergy * 128 + 127 - x.lane : -1;
-        key = wave_max(key);
-        if (key < 0) break;
+    while (x.hp > 0 && ballot(mine && x.menergy >= 80)) {   // no reduction once nobody can act
+        const int key = wave_max(mine && x.menergy >= 80 ? x.menergy * 128 + 127 - x.lane : -1);
         act(x, 127 - (key & 127));
     }
 }

@@ -609,10 +609,8 @@ __device__ __forceinline__ void primitive_learn(LCtx &c, int d, int limit, POut 
         for (int k = 0; k < 6; k++) maxspeed = imax(maxspeed, cf->kinds[k].speed);
         uint64_t movers = ballot(alive && x.mawake && x.menergy >= 80 && cheb(x.mpos, x.player) > 1);
         if (movers) bfs(x, movers, imax(2, (maxspeed + 9) / 10));
-        while (x.hp > 0) {
-            int key = (x.lane < REQ && x.menergy >= 80) ? x.menergy * 128 + 127 - x.lane : -1;
-            key = wave_max(key);
-            if (key < 0) break;
+        while (x.hp > 0 && ballot(x.lane < REQ && x.menergy >= 80)) {   // no reduction once nobody can act
+            const int key = wave_max(x.lane < REQ && x.menergy >= 80 ? x.menergy * 128 + 127 - x.lane : -1);
             int id = 127 - (key & 127);
             act(x, id);
             if (!(o.saw_enemy && o.saw_awake) && in_view(x, lane_val(x.mpos, id))) {   // nothing left to learn once both are set
