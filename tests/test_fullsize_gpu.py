@@ -59,6 +59,41 @@ def test_c5_full_size_slice(pkg):
     assert run(pkg, pkg.stress_config(), 262144, 2048, 256, 16) > 0
 
 
+def test_c5_ar_head_workload(pkg):
+    """C5's bench workload (bench.py --mode stress): the stress layout driven by the
+    autoregressive verb x target head through its HIP sampler, whose actions include waits,
+    REST, stairs and unreachable targets (-1) besides moves and attacks. 8,192 worlds x 96
+    steps; the first 2,048 are replayed on the host with the same actions (hash and out every
+    step, observations every 16th)."""
+    P = importlib.import_module('dcss-auto_amd.policy')
+    cfg = pkg.stress_config()
+    n, n_cpu, steps = 8192, 2048, 96
+    gpu = pkg.Env(n, cfg, seed=3)
+    cpu = O.OracleEnv(n_cpu, cfg, seed=3, threads=16)
+    model = P.ARPolicy(seed=0).cuda().to(torch.bfloat16)
+    seen, dones = set(), 0
+    for k in range(steps):
+        with torch.no_grad():
+            vl, tl, _ = model(gpu.obs)
+        _, _, a, _ = P.sample_ar(vl, tl, 11, k)
+        an = a.cpu().numpy()
+        seen.update(np.unique(an[:n_cpu]).tolist())
+        gpu.step(a)
+        cpu.step(an[:n_cpu])
+        dones += int(cpu.out[:, 1].sum())
+        if k % 32 == 0:
+            print(f'[c5 ar] step {k}', flush=True)
+        torch.cuda.synchronize()
+        gh = gpu.hash[:n_cpu].cpu().numpy().view(np.uint32)
+        assert np.array_equal(gh, cpu.hash), f'hash differs at step {k}: {np.flatnonzero(gh != cpu.hash)[:8]}'
+        go = gpu.out[:n_cpu].cpu().numpy()
+        assert np.array_equal(go.view(np.uint32), cpu.out.view(np.uint32)), f'out differs at step {k}'
+        if k % 16 == 0 or k == steps - 1:
+            assert np.array_equal(gpu.obs[:n_cpu].cpu().numpy(), cpu.obs), f'observation differs at step {k}'
+    assert {-1, 16, 17, 18} <= seen, sorted(seen)   # every non-move kind of action occurred
+    assert dones > 0
+
+
 def test_c3_full_size(pkg):
     """C3: 65,536 worlds x 128 steps of env step + observation + the fused bf16 policy forward
     with the counter-RNG sample, the sampled actions driving the env. The first 2,048 worlds
