@@ -580,10 +580,10 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
 // run on an otherwise idle chip (k_step 193 -> 187 us at 65,536 worlds). WPB is 4 for the
 // <= 8 monster build (0.176 -> 0.171 ms at 65,536 worlds) and 2 for the crowded build,
 // whose long serial worlds gain nothing from it.
-constexpr int STEP_TAIL = 8192, STEP_WPB = 4, CROWD_WPB = 2;
+constexpr int STEP_TAIL = 8192, STEP_WPB = 4, CROWD_WPB = 3;
 __host__ __device__ inline int step_groups(int n, int wpb) { return (n - (n < STEP_TAIL ? n : STEP_TAIL)) / wpb; }
 __host__ __device__ inline int step_blocks(int n, int wpb) { const int g = step_groups(n, wpb); return g + (n - wpb * g); }
-template <int RM, int WPB>
+template <int RM, int WPB, bool CROWD>
 __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int max_m, size_t row_bytes,
                                             const D1Config *cfgp, const D1Tables &tab, const int64_t *actions,
                                             uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
@@ -591,7 +591,7 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
     const int first = blk < g ? WPB * blk : WPB * g + (blk - g), last = imin(n, blk < g ? first + WPB : first + 1);
     Ctx x;
     x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
-    x.view_lds = WPB == CROWD_WPB;   // the crowded build keeps the player view in LDS
+    x.view_lds = CROWD;   // the crowded build keeps the player view in LDS
     Pre pf;
     prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
     for (int env = first; env < last; env++) {
@@ -648,14 +648,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __shared__ D1Config lcfg;
     for (int i = lane_id(); i < (int)(sizeof(D1Config) / 4); i += 64) ((uint32_t *)&lcfg)[i] = ((const uint32_t *)&cfg)[i];
     __syncthreads();
-    step_worlds<RM, STEP_WPB>(sm, state, n, max_m, row_bytes, &lcfg, tab, actions, obs, out, hash, active);
+    step_worlds<RM, STEP_WPB, false>(sm, state, n, max_m, row_bytes, &lcfg, tab, actions, obs, out, hash, active);
 }
 template <int RM>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_step_crowd(
     uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
     uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
-    step_worlds<RM, CROWD_WPB>(sm, state, n, max_m, row_bytes, &cfg, tab, actions, obs, out, hash, active);
+    step_worlds<RM, CROWD_WPB, true>(sm, state, n, max_m, row_bytes, &cfg, tab, actions, obs, out, hash, active);
 }
 
 // ---------------------------------------------------------------- monster-wait workload
