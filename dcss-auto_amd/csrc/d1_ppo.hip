@@ -46,7 +46,7 @@ constexpr int BP = 544;               // bias partial row: db1[256] | db2[256] |
 constexpr int C1 = 29;                // layer-1 K chunks (28 of 64 + the 8 inputs 1792..1799)
 constexpr int XB = 57;                // 32-row blocks of the x copy (1824 rows, 1800..1823 zero)
 constexpr int KW = 1024;              // samples per dW1 / dW2 workgroup
-constexpr int KW3 = 256;              // samples per dW3 / dW1-tail slice (one per dW2 workgroup)
+constexpr int KW3 = 256;              // samples per dW3 / dW1-tail slice (one workgroup each)
 constexpr int NT1 = 28;               // dW1 column tiles of 64 (inputs 0..1791; 1792..1799 are the tail)
 constexpr int NRF = (H * NT1 * 64 + H * H) / 4 / 256;   // k_reduce workgroups of mb/KW-partial units (dW1 columns
                                                        // < 1792, dW2), one unit of four elements per lane
@@ -552,9 +552,10 @@ __device__ __forceinline__ void wgrad_tile2(const uint16_t *at, const void *bt, 
     }
 }
 
-// Grouped launch of 32 * mb/KW workgroups (one per CU at mb = 8192):
-// [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW splits, each also
-// taking one mb/KW3 slice of dW3 and of the dW1 tail]. dW1[n1][f] = sum_m dh1[m][n1] x[m][f];
+// Grouped launch of 32 * mb/KW + mb/KW3 workgroups (288 at mb = 8192, up to two per CU):
+// [dW1: NT1 column tiles x mb/KW splits][dW2: 4 column tiles x mb/KW splits][mb/KW3 slices
+// of dW3 and of the dW1 tail]. The slices had ridden on the dW2 workgroups, which then
+// finished last; on their own they run beside the tiles (update 0.2474 -> 0.2434 s at C4). dW1[n1][f] = sum_m dh1[m][n1] x[m][f];
 // dW2[n2][n1] = sum_m dh2[m][n2] h1[m][n1]; dW3[j][n] = sum_m dz[m][j] h2[m][n]. Each writes
 // fp32 partials [split][rows][cols]. The dW1 splits of one column tile are consecutive
 // blocks, which a launch spreads over the eight XCDs, so each XCD's L2 serves one sample
@@ -581,7 +582,7 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
         return;
     }
     b -= NT1 * s1;
-    {
+    if (b < 4 * s1) {
         const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
         wgrad_tile2<false>(w.dh2f, w.h1f, 2 * tile, 8, nch, split * (KW / 64), KW / 64, bl, acc);
@@ -593,7 +594,9 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
 #pragma unroll
                 for (int r = 0; r < 16; r++)
                     out[(size_t)(64 * wave + 32 * i + drow(r, lh)) * H + 64 * tile + 32 * bb + lr] = acc[i][bb][r];
+        return;
     }
+    b -= 4 * s1;
     // slice b of dW3 (wave w: columns 64w..64w+63) and of the dW1 tail (wave w: rows
     // 64w..64w+63 against x^T block 56, inputs 1792..1823, of which 1792..1799 are kept)
     {
@@ -911,7 +914,7 @@ static void launch_pack(const D1PPOStep &a, const Work &w, hipStream_t st) {
 static void launch_step(const D1PPOStep &a, const Work &w, hipStream_t st) {
     const int s1 = a.mb / KW;
     hipLaunchKernelGGL(k_rows, dim3(a.mb / R), dim3(512), 0, st, a, w);
-    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1), dim3(256), 0, st, a, w);
+    hipLaunchKernelGGL(k_wgrad, dim3(NT1 * s1 + 4 * s1 + a.mb / KW3), dim3(256), 0, st, a, w);
     hipLaunchKernelGGL(k_reduce, dim3(NRED + NBIASB), dim3(256), 0, st, a, w);
     const int64_t nadam = (a.nparams / 4 + 255) / 256;   // one group of four parameters per lane
     hipLaunchKernelGGL(k_adam, dim3((unsigned)nadam), dim3(256), 0, st, a, w);
