@@ -26,7 +26,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-# Algorithmic bytes per env step at 8 monsters: obs 1800 +
+# Algorithmic bytes per env step at 8 monsters (what one step must read or write): obs 1800 +
 # action 1 + reward/done/hash 9 + 2 x (24 + 7 x 8) dynamic state + 600 seen/viewed band
 # + 700 level bitmap.
 STEP_BYTES = {8: 3270, 40: 3718}
