@@ -578,8 +578,8 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
 // last STEP_TAIL worlds, one per workgroup: the workgroups dispatched last then hold one
 // world, which shortens the tail in which a few slow worlds (resets, long monster turns)
 // run on an otherwise idle chip (k_step 193 -> 187 us at 65,536 worlds). WPB is 4 for the
-// <= 8 monster build (0.176 -> 0.171 ms at 65,536 worlds) and 2 for the crowded build,
-// whose long serial worlds gain nothing from it.
+// <= 8 monster build (0.176 -> 0.171 ms at 65,536 worlds) and 3 for the crowded build
+// (C5 k_step: 2 worlds 3.38 ms, 3 worlds 3.35, 4 worlds 3.37).
 constexpr int STEP_TAIL = 8192, STEP_WPB = 4, CROWD_WPB = 3;
 __host__ __device__ inline int step_groups(int n, int wpb) { return (n - (n < STEP_TAIL ? n : STEP_TAIL)) / wpb; }
 __host__ __device__ inline int step_blocks(int n, int wpb) { const int g = step_groups(n, wpb); return g + (n - wpb * g); }

@@ -921,8 +921,9 @@ static void launch_step(const D1PPOStep &a, const Work &w, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------- library-owned work buffer
-// d1_ppo_step_static's work buffer: one per GPU, held from the first use until the process
-// ends, sized for the largest minibatch it accepts. In host code `scratch` names a host-side
+// d1_ppo_step_static's work buffer: one per GPU, reserved when the code object is loaded on
+// that device (every process that loads this library holds it, whether or not it calls the
+// PPO step) until the process ends, sized for the largest minibatch it accepts. In host code `scratch` names a host-side
 // stand-in, never the device array: the device address comes from hipGetSymbolAddress, once
 // per device, with that device current.
 constexpr size_t SCRATCH_BYTES = layout(D1_PPO_STATIC_MAX_MB).total;

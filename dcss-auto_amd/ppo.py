@@ -182,9 +182,11 @@ class FastPPO:
 
     def record_head(self, on=True):
         """Have every following minibatch step write the head outputs its loss was computed
-        from (16 logits + value, bf16-rounded, as fp32) into self.head_out [minibatch, 17].
-        Steps already captured in a graph keep the setting they were captured with."""
-        self.head_out = torch.empty((self.minibatch, 17), dtype=torch.float32, device=self.dev) if on else None
+        from (16 logits + value, bf16-rounded, as fp32) into self.head_out [minibatch, 17]
+        (NaN until a step writes it). A captured graph holds the buffer it was captured
+        with, so this drops it and the next update captures again."""
+        self._g = self._g_buf = None
+        self.head_out = torch.full((self.minibatch, 17), float('nan'), device=self.dev) if on else None
 
     def set_order(self, perm):
         """Sample order of the next minibatches (int64 [n] on the device); resets the cursor

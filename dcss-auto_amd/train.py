@@ -29,6 +29,11 @@ from . import _lib
 from . import policy as P
 from . import ppo as ppo_mod
 
+# Checkpoint layout version: 2 added the trainer-settings record and grew crowded env state
+# rows (more than 8 monsters) by the 2,656-byte distance-field memo; version-1 files carry no
+# 'format' key.
+CHECKPOINT_FORMAT = 2
+
 
 class Trainer:
     def __init__(self, env, model, horizon=128, minibatch=8192, epochs=4, lr=3e-4, eps=1e-5, clip=0.2,
@@ -163,10 +168,14 @@ class Trainer:
         return dict(p=cpu(F.p), pb=cpu(F.pb), m=cpu(F.m), v=cpu(F.v), adam_step=cpu(self.ppo.step_t),
                     env_state=cpu(self.env.state), next_obs=cpu(self.next_obs), t=cpu(self.t_dev),
                     gen=self.gen.get_state(), updates=torch.tensor(self.updates), decisions=torch.tensor(self.decisions),
-                    hparams=dict(self.hparams))
+                    hparams=dict(self.hparams), format=CHECKPOINT_FORMAT)
 
     def load_state_dict(self, sd):
         F = self.ppo.flat
+        if sd.get('format') != CHECKPOINT_FORMAT:
+            raise ValueError(f"checkpoint format {sd.get('format', 1)} is not this trainer's ({CHECKPOINT_FORMAT}): "
+                             'it was written by an older version (no settings record; env state rows of '
+                             'crowded layouts without the distance-field memo) and cannot be resumed')
         saved = sd.get('hparams')
         if saved != self.hparams:
             diff = sorted(k for k in set(self.hparams) | set(saved or {})

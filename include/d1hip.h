@@ -259,7 +259,9 @@ int d1_ppo_step(const D1PPOStep *s, void *stream);
  * one call equals d1_ppo_prepare + d1_ppo_step on a private work buffer, bit for bit.
  * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU
  * (two streams, two threads) race and give undefined results; calls in stream order do not.
- * The call itself allocates nothing (no hipMalloc, no library allocation). */
+ * The call itself allocates nothing (no hipMalloc, no library allocation). Its first call on
+ * a device resolves that device's array address (hipGetSymbolAddress), which is not a stream
+ * operation: make that first call outside stream capture; later calls may be captured. */
 #define D1_PPO_STATIC_MAX_MB 8192
 #define D1_E_SCRATCH (-4)             /* request larger than the library-owned buffer */
 int d1_ppo_step_static(const D1PPOStep *s, void *stream);

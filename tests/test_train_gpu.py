@@ -22,7 +22,7 @@ def make_trainer(pkg, graph, n=2048, T=8, seed=11):
 def assert_same_state(a, b):
     assert a.keys() == b.keys()
     for key in a:
-        if key == 'hparams':
+        if key in ('hparams', 'format'):
             assert a[key] == b[key]
         else:
             assert torch.equal(a[key], b[key]), key

@@ -88,3 +88,46 @@ def test_static_step_refuses_oversize_minibatch():
     args = _lib.D1PPOStep(mb=16384, n=32768)
     assert _lib.load().d1_ppo_step_static(C.byref(args), None) == -4   # D1_E_SCRATCH, nothing launched
     assert _lib.load().d1_ppo_step_static(None, None) == -1
+
+
+def test_static_step_allocates_nothing_and_replays_from_a_graph():
+    """After its first call on the device (made outside capture, as the header requires), a
+    static call leaves the device's free memory unchanged, and static calls captured in a HIP
+    graph replay equal to eager d1_ppo_prepare + d1_ppo_step calls, bit for bit, with eager
+    torch work between the replays."""
+    _lib = importlib.import_module('dcss-auto_amd._lib')
+    lib = _lib.load()
+    ref, new = _pair(4096)
+    buf = _buffer(6, 4096, seed=9)   # six minibatches: two eager steps, then three replays
+    perm = torch.randperm(6 * 4096, device='cuda', generator=torch.Generator(device='cuda').manual_seed(3))
+    adv, ret = ref.advantages(buf)
+    obs, actions, logp = ref._views(buf)
+    for fast in (ref, new):
+        fast.set_order(perm)
+    new._packed = True
+    args = new._struct(obs, actions, logp, adv, ret)
+    args.work, args.work_bytes = None, 0
+    print('[no-alloc] first static call (outside capture)', flush=True)
+    ref._step(obs, actions, logp, adv, ret)
+    _lib.check(lib.d1_ppo_step_static(C.byref(args), torch.cuda.current_stream().cuda_stream), 'static')
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    ref._step(obs, actions, logp, adv, ret)
+    _lib.check(lib.d1_ppo_step_static(C.byref(args), torch.cuda.current_stream().cuda_stream), 'static')
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0, 'a static call changed the free device memory'
+    want, got = _outputs(ref), _outputs(new)
+    for name in want:
+        assert torch.equal(want[name], got[name]), ('eager', name)
+    print('[no-alloc] capture', flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.check(lib.d1_ppo_step_static(C.byref(args), torch.cuda.current_stream().cuda_stream), 'static')
+    for r in range(3):
+        ref._step(obs, actions, logp, adv, ret)
+        g.replay()
+        torch.cuda.synchronize()
+        assert float(adv.abs().sum()) > 0   # eager reductions between the replays
+        want, got = _outputs(ref), _outputs(new)
+        for name in want:
+            assert torch.equal(want[name], got[name]), ('replay', r, name)
