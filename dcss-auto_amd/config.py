@@ -137,11 +137,15 @@ def reference_config(count=24, *, stairs=3, wake_los=1, clear_on_kill_all=0):
                        turn_cost=1e-5, limit=2048)
 
 
-def v1_config(count=8):
-    """The v1 floor-clear task of gpu-d1/src/learn.cu with SLEEP_ON, EXPLORE_REWARD and
-    MARK_WALLS on map 1057: kill-all clears, Chebyshev waking, no stairs, 256 turns."""
-    return make_config(count, rng_mode=RNG_PCG, level_mode=LEVEL_SHARED, roster_mode=0, awake_pct=0,
-                       wake_los=0, stairs=0, clear_on_kill_all=1, limit=256)
+def v1_config(count=8, sleep=True):
+    """The v1 floor-clear task of gpu-d1/src/learn.cu on map 1057: kill-all clears, no
+    stairs, 256 turns. sleep=True is its SLEEP_ON + EXPLORE_REWARD + MARK_WALLS build
+    (monsters start asleep and wake within Chebyshev 6); sleep=False is the default build
+    (gpu-d1/Makefile:14-16, no defines: every monster awake from the start, rewards -0.001
+    per turn, +1 per kill, +3 on clear, -1 on death, no exploration reward)."""
+    return make_config(count, rng_mode=RNG_PCG, level_mode=LEVEL_SHARED, roster_mode=0,
+                       awake_pct=0 if sleep else 100, wake_los=0, stairs=0, clear_on_kill_all=1, limit=256,
+                       explore_milli=2 if sleep else 0)
 
 
 def shared_map_arrays():

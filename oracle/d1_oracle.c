@@ -11,6 +11,11 @@
  * observation and the state hash. It is the checker for the HIP library; the
  * product never links it. Compile with -ffp-contract=off (reward arithmetic is
  * compared bit for bit).
+ *
+ * Parity unpinned: reset's stairs reservoir (draws from an RNG copy after the monster
+ * draws), pinned by its postconditions only. The v1 reset draw order, the transition and
+ * the v1 controller are pinned by the reference's own recorded v1 run
+ * (gpu-d1/results/learning-v1-tests.log:1-3, tests/test_v1_reference_run.py).
  */
 #include "d1_oracle.h"
 #include <stddef.h>
@@ -292,6 +297,12 @@ static int visible_awake(const OState *s, const D1Config *c) {
     return 0;
 }
 
+/* Planted mistakes for the tests that show a fixture bites (0 = none, the faithful rules):
+ * 1 a monster's energy drawn before its cell at reset, 2 the v1 controller's HP and
+ * distance ties kept by the later candidate, 3 the player's melee damage 1 + r(5). */
+static int planted;
+void o_plant(int which) { planted = which; }
+
 /* gpu-d1/branches/d1-stairs-v2/src/learn.cu:351-446 with the v1 roster
  * (gpu-d1/src/learn.cu:305-314); roster_mode 1 and awake_pct are build extensions
  * whose draws follow the energy draw. Clumped/ogre placement is not modelled. */
@@ -303,7 +314,7 @@ static void reset(OState *s, const D1Config *c) {
     s->hp = c->hp; s->regen = 0; s->blocks = 0;
     s->ticks = 0; s->decisions = 0; s->killed = 0; s->floor_seen = 0;
     for (int i = 0; i < c->count; i++) {
-        int p, tries = 0;
+        int p, tries = 0, early = planted == 1 ? rng_r(g, 10) : -1;
         do { p = s->cells[rng_r(g, s->ncells)]; } while ((p == s->player || s->occ[p] >= 0) && ++tries < 65536);
         /* The reference retries without bound; the cap (never reached with >= 72 cells
          * and <= 64 monsters) bounds the GPU loop, falling back to the first free cell. */
@@ -312,7 +323,7 @@ static void reset(OState *s, const D1Config *c) {
         s->pos[i] = (int16_t)p;
         s->occ[p] = (int16_t)i;
         if (c->roster_mode == 0) { s->kind[i] = (uint8_t)(i % 6); s->mhp[i] = (int16_t)MHP[i % 6]; }
-        s->energy[i] = (int16_t)(70 + rng_r(g, 10));
+        s->energy[i] = (int16_t)(70 + (early >= 0 ? early : rng_r(g, 10)));
         if (c->roster_mode == 1) {
             s->kind[i] = (uint8_t)rng_r(g, 6);
             s->mhp[i] = (int16_t)(c->hp_lo + rng_r(g, c->hp_hi - c->hp_lo + 1));
@@ -429,14 +440,14 @@ static OMonsters env_monsters(OState *s, const D1Config *c) {
                    c->repair, c->gdr[0], c->gdr[1]};
     return m;
 }
-/* Distance-from-player field over floor, 8-neighbour BFS (what the reference's
- * all-pairs table rows hold, gpu-d1/scripts/learn_env.py:31-39). */
-static void player_field(const OState *s, uint16_t *ds) {
+/* Distance field from `source` over floor, 8-neighbour BFS (what the reference's all-pairs
+ * table rows hold, gpu-d1/scripts/learn_env.py:31-39); 65535 = unreached. */
+static void floor_field(const OState *s, int source, uint16_t *ds) {
     static __thread int16_t queue[N];
     for (int p = 0; p < N; p++) ds[p] = 65535;
     int head = 0, tail = 1;
-    queue[0] = (int16_t)s->player;
-    ds[s->player] = 0;
+    queue[0] = (int16_t)source;
+    ds[source] = 0;
     while (head < tail) {
         int p = queue[head++];
         for (int d = 0; d < 8; d++) {
@@ -445,6 +456,7 @@ static void player_field(const OState *s, uint16_t *ds) {
         }
     }
 }
+static void player_field(const OState *s, uint16_t *ds) { floor_field(s, s->player, ds); }
 /* LOS-gated waking, gpu-d1/branches/d1-stairs-v2/src/learn.cu:201-207; the v1
  * rule is Chebyshev <= 6 alone (gpu-d1/src/learn.cu:555-559). */
 static int detects(const OState *s, const D1Config *c, int origin) {
@@ -467,7 +479,7 @@ static void primitive(OState *s, const D1Config *c, int d, float *out8, int *saw
             int id = s->occ[p];
             if (id >= 0) {
                 if (rng_r(&s->rng, 5) != 0) {
-                    s->mhp[id] = (int16_t)(s->mhp[id] - (1 + rng_r(&s->rng, 4)));
+                    s->mhp[id] = (int16_t)(s->mhp[id] - (1 + rng_r(&s->rng, planted == 3 ? 5 : 4)));
                     if (s->mhp[id] <= 0) {
                         s->mhp[id] = 0; s->occ[p] = -1; s->energy[id] = -30000;
                         s->killed++;
@@ -751,6 +763,41 @@ int o_wait_run(int count, int steps, int heap, int scenario_fixture, uint64_t se
  * gpu-d1/branches/d1-stairs-v2/src/learn.cu:876-888): descend on a stair, else attack
  * the weakest visible adjacent monster, else step along the true distance field
  * toward the nearest living monster, else wait. */
+/* gpu-d1/src/learn.cu:599-621, the v1 task's pursuit controller and the action stream of its
+ * parity run (gpu-d1/scripts/test_learning.py:48). Returns a v1 action: direction 0-7 (move,
+ * or melee when the cell holds a monster) or 8 (wait). The living adjacent monster with the
+ * least HP first, a strictly lower HP replacing the choice, so ties keep the earlier direction;
+ * else the living monster nearest to the player by floor distance (strictly nearer replaces:
+ * ties keep the lowest id), then the neighbouring floor cell with the least distance to that
+ * monster's cell among those strictly closer than the player's own (earlier directions win
+ * ties); 8 when no monster lives or no neighbour is closer. */
+int o_heuristic_v1(OState *s, const D1Config *c) {
+    static __thread uint16_t dist[N];
+    int best = -1, bhp = 10000;
+    for (int d = 0; d < 8; d++) {
+        int p = neighbor(s->player, d);
+        if (p >= 0 && s->occ[p] >= 0 && (s->mhp[s->occ[p]] < bhp || (planted == 2 && s->mhp[s->occ[p]] == bhp))) {
+            bhp = s->mhp[s->occ[p]]; best = d;
+        }
+    }
+    if (best >= 0) return best;
+    player_field(s, dist);
+    int target = -1, bd = 65535;
+    for (int i = 0; i < c->count; i++)
+        if (s->mhp[i] > 0 && (dist[s->pos[i]] < bd || (planted == 2 && dist[s->pos[i]] == bd))) {
+            bd = dist[s->pos[i]]; target = s->pos[i];
+        }
+    if (target < 0) return 8;
+    floor_field(s, target, dist);
+    const int own = dist[s->player];
+    bd = own;
+    best = 8;
+    for (int d = 0; d < 8; d++) {
+        int p = neighbor(s->player, d);
+        if (floor_at(s, p) && (dist[p] < bd || (planted == 2 && dist[p] == bd && dist[p] < own))) { bd = dist[p]; best = d; }
+    }
+    return best;
+}
 int o_heuristic(OState *s, const D1Config *c) {
     static __thread uint16_t dist[N];
     if (stair_index(s) > 0) return 18;

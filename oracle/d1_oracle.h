@@ -98,6 +98,8 @@ int o_step(OState *st, int n, const D1Config *c, const int64_t *actions, uint8_t
 void o_obs(const OState *s, const D1Config *c, uint8_t *obs);
 uint32_t o_hash(const OState *s, const D1Config *c);
 int o_heuristic(OState *s, const D1Config *c);
+int o_heuristic_v1(OState *s, const D1Config *c);                      /* learn.cu:599-621 */
+void o_plant(int which);   /* planted mistakes for tests (d1_oracle.c); 0 = the faithful rules */
 int o_field_offset(int k);
 void o_world_map(OState *s, const uint8_t *floor, const uint8_t *cells);
 void o_reset(OState *s, const D1Config *c);

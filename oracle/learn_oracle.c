@@ -13,6 +13,11 @@
  * all-pairs rows as the reference does; the HIP library recomputes it by BFS, so
  * agreement also checks that substitution. Compile with -ffp-contract=off.
  * Only tests/ load this; the product never links it.
+ *
+ * Parity unpinned (followed by reading only; no reference log or fixture fixes them):
+ * lo_reset's clump anchors and stairs reservoir (draws from RNG copies; the player and
+ * monster draws before them are the v1 order that the reference's recorded v1 run pins),
+ * and lo_heuristic_one's priority order between its rules (each rule is pinned on its own).
  */
 #include "d1_oracle.h"
 #include "../include/d1learn.h"

@@ -77,9 +77,16 @@ class OracleEnv:
         return np.array([self.L.o_heuristic(self.state[i:].ctypes.data, C.byref(self.cfg)) for i in range(self.batch)],
                         np.int64) if n else None
 
-    def fields(self):
-        """Structured copy of the worlds (OState, oracle/d1_oracle.h)."""
-        return self.state.reshape(-1).view(ostate_dtype()).copy()
+    def heuristic_v1(self):
+        """The v1 pursuit controller (o_heuristic_v1): v1 actions 0-8, one per world."""
+        self.L.o_heuristic_v1.argtypes = [C.c_void_p, C.c_void_p]
+        return np.array([self.L.o_heuristic_v1(self.state[i:].ctypes.data, C.byref(self.cfg))
+                         for i in range(self.batch)], np.int64)
+
+    def fields(self, worlds=None):
+        """Structured copy of the worlds (OState, oracle/d1_oracle.h): all, or a slice."""
+        rows = self.state if worlds is None else self.state[worlds]
+        return np.ascontiguousarray(rows).reshape(-1).view(ostate_dtype()).copy()
 
 
 OSTATE_FIELDS = [('rng', 'u1', 48), ('env_id', '<u4'), ('t', '<u4'), ('episode', '<i4'), ('player', '<i4'),
