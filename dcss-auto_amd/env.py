@@ -17,6 +17,55 @@ import torch
 from . import _lib, config as cfgmod, data
 
 
+# The state row's 64-byte header (d1_env.hip `Hdr`), little-endian and packed.
+HEADER = np.dtype([('rng_state', '<u8'), ('rng_inc', '<u8'), ('env_id', '<u4'), ('t', '<u4'), ('episode', '<i4'),
+                   ('player', '<i2'), ('hp', '<i2'), ('regen', '<i2'), ('ncells', '<i2'), ('ticks', '<i4'),
+                   ('killed', '<i4'), ('decisions', '<i4'), ('floor_seen', '<i4'), ('stairs', '<i2', 3),
+                   ('blocks', '<i2'), ('first_stair_tick', '<i4')])
+assert HEADER.itemsize == 64
+
+
+def _bitmap_bytes(words):
+    """[n, 840] bytes of 70 rows x 3 little-endian dwords (bit x of row y) -> [n, 5600] 0/1."""
+    bits = np.unpackbits(words.reshape(len(words), 70, 12), axis=2, bitorder='little')
+    return np.ascontiguousarray(bits[:, :, :80].reshape(len(words), 5600))
+
+
+def decode_rows(raw, max_monsters):
+    """State rows (uint8 [n, d1_state_bytes(max_monsters)], a host copy) -> one numpy record
+    per world: the header scalars (rng_state is the PCG state, or the Philox key in counter
+    mode), `view` [15, 15] (the player's field of view the row memoises, [dy+7][dx+7]), the
+    monster fields pos/mhp/energy/awake/kind [max_monsters], and the `viewed`, `floor` and
+    `cells` (spawnable) maps as [5600] bytes of 0/1. The rows of crowded layouts also carry a
+    distance-field memo, which is a cache and is not decoded."""
+    raw = np.ascontiguousarray(raw, np.uint8)
+    n, m = len(raw), max_monsters
+    dt = np.dtype(HEADER.descr + [('view', 'u1', (15, 15)), ('pos', '<i2', m), ('mhp', '<i2', m),
+                                   ('energy', '<i2', m), ('awake', 'u1', m), ('kind', 'u1', m),
+                                   ('viewed', 'u1', 5600), ('floor', 'u1', 5600), ('cells', 'u1', 5600)])
+    out = np.zeros(n, dt)
+    hdr = raw[:, :64].copy().view(HEADER).reshape(n)
+    for name in HEADER.names:
+        out[name] = hdr[name]
+    quads = raw[:, 64:96].copy().view('<u8')                  # quadrants (+x,+y) (-x,+y) (-x,-y) (+x,-y)
+    j = np.arange(64, dtype=np.uint64)
+    tx, ty = (j % 8).astype(int), (j // 8).astype(int)
+    for q, (sx, sy) in enumerate(((1, 1), (-1, 1), (-1, -1), (1, -1))):
+        on = ((quads[:, q, None] >> j) & np.uint64(1)).astype(np.uint8)   # [n, 64]
+        out['view'][:, sy * ty + 7, sx * tx + 7] |= on
+    mon = raw[:, 96:96 + 8 * m].copy().reshape(n, m, 8)
+    out['pos'] = mon[:, :, 0:2].copy().view('<i2')[..., 0]
+    out['mhp'] = mon[:, :, 2:4].copy().view('<i2')[..., 0]
+    out['energy'] = mon[:, :, 4:6].copy().view('<i2')[..., 0]
+    out['awake'] = mon[:, :, 6]
+    out['kind'] = mon[:, :, 7]
+    o = 96 + 8 * m
+    for name in ('viewed', 'floor', 'cells'):
+        out[name] = _bitmap_bytes(raw[:, o:o + 840])
+        o += 840
+    return out
+
+
 class Env:
     def __init__(self, batch=512, cfg=None, seed=0, device='cuda', max_monsters=None, hash=True):
         self.with_hash = hash
@@ -48,9 +97,14 @@ class Env:
         state rows (the 840-byte floor bitmap after the header, view, monsters and
         viewed bitmap)."""
         off = 96 + 8 * self.max_monsters + 840
-        words = self.state[:, off:off + 840].cpu().numpy().view('<u4').reshape(self.batch, 70, 3)
-        bits = np.unpackbits(words.view(np.uint8).reshape(self.batch, 70, 12), axis=2, bitorder='little')
-        return np.ascontiguousarray(bits[:, :, :80].reshape(self.batch, 5600))
+        return _bitmap_bytes(self.state[:, off:off + 840].cpu().numpy())
+
+    def fields(self, worlds=None):
+        """The worlds' state rows decoded on the host (decode_rows), all of them or the slice
+        or index array `worlds`; the reference's tests read its rows the same way through a
+        ctypes mirror of `State` (gpu-d1/scripts/test_learning.py:15-36)."""
+        rows = self.state if worlds is None else self.state[worlds]
+        return decode_rows(rows.cpu().numpy(), self.max_monsters)
 
     @property
     def stream(self):

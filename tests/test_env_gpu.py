@@ -1,9 +1,11 @@
-"""HIP environment vs the CPU oracle: per-step state hash, out[] and the uint8
-observation must be identical (integer/byte work is bit-exact; reward floats too)."""
+"""HIP environment vs the CPU oracle: per-step state hash, out[], the uint8 observation
+and every field of the state rows must be identical (integer/byte work is bit-exact;
+reward floats too)."""
 import numpy as np
 import pytest
 import torch
 
+from envstate import assert_same_worlds
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -41,6 +43,7 @@ def compare(gpu, cpu, step, name):
             msg += f' obs diffs (dy,dx,ch) {d.tolist()} gpu {[int(go[e][tuple(i)]) for i in d]} ' \
                    f'cpu {[int(cpu.obs[e][tuple(i)]) for i in d]}'
         pytest.fail(msg)
+    assert_same_worlds(gpu.fields(), cpu.fields(), gpu.cfg, obs=go, label=f'{name} step {step}')
 
 
 @pytest.mark.parametrize('name,spec,batch,steps,nact', CASES)

@@ -6,15 +6,21 @@ every world, the uint8 observation every step (C1) or every 8th step (C2). C3 an
 at their full sizes on the GPU (65,536 worlds x 128 steps with the bf16 policy choosing
 the actions; 262,144 worlds x 256 steps with 40 monsters); worlds are independent and keyed
 by their index, so the first 2,048 of them are replayed on the host and compared (hash and
-out every step, observations every 8th / 16th). Actions: uniform over the 16 semantic
-actions from a seeded stream (C1, C2, C5), or the fused policy's samples (C3)."""
+out every step, observations every 8th / 16th). Every 8th step the decoded state rows of the
+compared worlds (the first 2,048 in C2) are checked field by field as well
+(tests/envstate.py). Actions: uniform over the 16 semantic actions from a seeded stream (C1,
+C2, C5), or the fused policy's samples (C3)."""
 import importlib
 
 import numpy as np
 import pytest
 import torch
 
+from envstate import assert_same_worlds
 from oracle import oracle as O
+
+STATE_EVERY = 8
+STATE_WORLDS = 2048
 
 pytestmark = pytest.mark.gpu
 
@@ -40,6 +46,10 @@ def run(pkg, cfg, n_gpu, n_cpu, steps, obs_every, seed=2026):
             assert np.array_equal(go.view(np.uint32), cpu.out.view(np.uint32)), f'out differs at step {k}'
         if k % obs_every == 0 or k == steps - 1:
             assert np.array_equal(gpu.obs[:n_cpu].cpu().numpy(), cpu.obs), f'observation differs at step {k}'
+        if k % STATE_EVERY == 0 or k == steps - 1:
+            m = min(n_cpu, STATE_WORLDS)
+            assert_same_worlds(gpu.fields(slice(0, m)), cpu.fields(slice(0, m)), cfg,
+                               obs=gpu.obs[:m].cpu().numpy(), label=f'step {k}')
     return dones
 
 
@@ -90,6 +100,9 @@ def test_c5_ar_head_workload(pkg):
         assert np.array_equal(go.view(np.uint32), cpu.out.view(np.uint32)), f'out differs at step {k}'
         if k % 16 == 0 or k == steps - 1:
             assert np.array_equal(gpu.obs[:n_cpu].cpu().numpy(), cpu.obs), f'observation differs at step {k}'
+        if k % STATE_EVERY == 0 or k == steps - 1:
+            assert_same_worlds(gpu.fields(slice(0, n_cpu)), cpu.fields(), cfg,
+                               obs=gpu.obs[:n_cpu].cpu().numpy(), label=f'step {k}')
     assert {-1, 16, 17, 18} <= seen, sorted(seen)   # every non-move kind of action occurred
     assert dones > 0
 
@@ -151,4 +164,6 @@ def test_c3_full_size(pkg):
         assert np.array_equal(go.view(np.uint32), cpu.out.view(np.uint32)), f'out differs at step {k}'
         if k % 8 == 0 or k == steps - 1:
             assert np.array_equal(gpu.obs[:n_cpu].cpu().numpy(), cpu.obs), f'observation differs at step {k}'
+            assert_same_worlds(gpu.fields(slice(0, n_cpu)), cpu.fields(), cfg,
+                               obs=gpu.obs[:n_cpu].cpu().numpy(), label=f'step {k}')
     assert dones > 0
