@@ -31,6 +31,9 @@ BF16_PEAK_TFLOPS = 2500.0
 # + 700 level bitmap.
 STEP_BYTES = {8: 3270, 40: 3718}
 TRUNK_FLOPS = 2 * (1800 * 256 + 256 * 256 + 256 * 17)
+# The autoregressive policy per sample: trunk, verb logits + value (9 outputs), the target
+# MLP's trunk part (64), and its output layer (25 x 64) for the drawn verb only
+AR_FLOPS = 2 * (1800 * 256 + 256 * 256 + 256 * 9 + 256 * 64 + 64 * 25)
 
 
 def measured_traffic(path=ROOT / 'profiles' / 'k_step_hbm_traffic.md'):
@@ -253,15 +256,20 @@ def roofline(kernel, achieved, launch_ms, step_bytes, traffic, launches):
 
 def stress_bench(args, envs=262144, horizon=256, warmup=4):
     """C5: 262,144 generated-level worlds with 40 monsters (HP U[40,60], half awake at
-    spawn), the bf16 trunk with the autoregressive verb(8) x target(25) head and the HIP
-    two-stage sampler, 256 steps. Reports decisions/s and k_step's algorithmic HBM rate."""
+    spawn), the bf16 trunk with the autoregressive verb(8) x target(25) head and its
+    two-stage counter-RNG draw fused into one kernel (d1_policy_fwd_sample_ar), 256 steps.
+    Reports decisions/s and k_step's algorithmic HBM rate."""
     import torch
     pkg = importlib.import_module('dcss-auto_amd')
     P = importlib.import_module('dcss-auto_amd.policy')
     dev = torch.device('cuda:0')
     env = pkg.Env(envs, pkg.stress_config(), seed=3, hash=False)
     model = P.ARPolicy(seed=0).to(dev).to(torch.bfloat16)
+    packed = model.packed()
     actions = torch.zeros(envs, dtype=torch.int64, device=dev)
+    logp = torch.empty(envs, device=dev)
+    value = torch.empty(envs, device=dev)
+    obs = env.obs.view(envs, -1)
 
     def one(t, ev=None):
         if ev is not None:
@@ -269,22 +277,22 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
         env.step(actions)
         if ev is not None:
             ev[1].record()
-        with torch.no_grad():
-            vl, tl, _ = model(env.obs)
-        _, _, a, _ = P.sample_ar(vl, tl, 11, t)
-        actions.copy_(a)
+        P.policy_fwd_sample_ar(obs, packed, 11, t, actions, logp, value)
+        if ev is not None:
+            ev[2].record()
 
     for t in range(warmup):
         one(t)
     torch.cuda.synchronize()
     every = event_stride(horizon)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(0, horizon, every)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, horizon, every)]
     t0 = time.perf_counter()
     for k in range(horizon):
         one(warmup + k, events[k // every] if k % every == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
+    policy_ms = sum(e[1].elapsed_time(e[2]) for e in events) / len(events)
     achieved = STEP_BYTES[40] * envs / (step_ms * 1e-3) / 1e9
     traffic = measured_traffic(ROOT / 'profiles' / 'k_step_c5_counters.md')
     return {'metric': 'env decisions/sec at 262,144 envs, 40 monsters, AR 8x25 head (C5)',
@@ -292,6 +300,8 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
             'ms_per_step': wall / horizon * 1e3,
             'config': {'workload': 'C5', 'envs': envs, 'monsters': 40, 'hp': [40, 60], 'awake_pct': 50,
                        'head': 'AR verb 8 x target 25', 'horizon': horizon},
+            'policy': {'kernel': 'd1t::k_policy<2> (trunk + AR head + two-stage draw)', 'avg_launch_ms': policy_ms,
+                       'mfma_tflops': AR_FLOPS * envs / (policy_ms * 1e-3) / 1e12},
             'roofline': roofline('d1::k_step', achieved, step_ms, STEP_BYTES[40], traffic, len(events))}
 
 

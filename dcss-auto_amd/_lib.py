@@ -12,7 +12,8 @@ SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd
            'd1_init', 'd1_step', 'd1_sample', 'd1_sample_dev', 'd1_gae', 'd1_obs_to_bf16', 'd1_obs_d4',
            'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step', 'd1_ppo_step_static', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
            'd1_sample_ar', 'd1_los_table', 'd1_distance_rows', 'd1_policy_packed_elems', 'd1_policy_pack',
-           'd1_policy_fwd', 'd1_policy_fwd_sample')
+           'd1_policy_fwd', 'd1_policy_fwd_sample', 'd1_policy_ar_packed_elems', 'd1_policy_ar_pack',
+           'd1_policy_fwd_sample_ar')
 LEARN_SYMBOLS = ('learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size',
                  'learn_action_size', 'learn_out_size', 'learn_config_bytes', 'learn_init', 'learn_step',
                  'learn_step_active', 'learn_heuristic')
@@ -66,6 +67,10 @@ def load():
         L.d1_policy_pack.argtypes = [p, p, p, p, p]
         L.d1_policy_fwd.argtypes = [p, i, p, p, p, p, p, p, p]
         L.d1_policy_fwd_sample.argtypes = [p, i, p, p, p, p, C.c_uint64, p, C.c_uint32, p, p, p, p, p]
+        L.d1_policy_ar_packed_elems.argtypes = []
+        L.d1_policy_ar_packed_elems.restype = C.c_int64
+        L.d1_policy_ar_pack.argtypes = [p, p, p, p, p, p, p, p]
+        L.d1_policy_fwd_sample_ar.argtypes = [p, i, p, p, p, p, p, C.c_uint64, p, C.c_uint32, p, p, p, p, p, p, p, p]
         _LIB = L
     return _LIB
 

@@ -45,22 +45,195 @@ constexpr int LDS_BYTES = LDS_W + 2 * 320 * 2;   // + biases b1 | b2 | head bias
 static_assert(2 * 2048 * 16 <= LDS_W, "W1 double buffer inside the staging area");
 static_assert(NSTAGE % 256 == 0, "whole staging rounds");
 
+// Autoregressive head (BASELINE C5, dcss-auto_amd/policy.py ARPolicy): the trunk head above
+// holds the verb logits (rows 0-7, rows 8-15 zero) and the value (row 16); the target MLP's
+// trunk part t1[:, :256] is two more 32-row head tiles, its verb-embedding part enters as the
+// table ev[verb][64] = t1[:, 256:] . embedding[verb] (bf16, computed by torch once per weight
+// update), and its output layer t2 (25 x 64) is one more MFMA tile over K = 64. The packed
+// buffer continues after PEND: the two t1 tiles [2][16 steps][64][8] in the head's K order,
+// t2 [4 steps][64][8] with hidden unit kperm(s, h, j), and ev [8][64].
+constexpr int NV = 8, NT = 25, TH = 64;
+constexpr int PA1 = PEND;                    // t1 trunk columns: 2 tiles x 16 steps
+constexpr int PA2 = PA1 + 2 * 16 * 512;      // t2: 4 steps, rows 25..31 zero
+constexpr int PAE = PA2 + 4 * 512;           // ev [8][64]
+constexpr int PAEND = PAE + NV * TH;
+constexpr int NSTAGE_AR = (PAEND - PA1) / 8; // 16-byte pieces restaged after layer 2 (2,368)
+constexpr int LDS_BYTES_AR = LDS_BYTES + (TH + 32) * 2;   // + t1 bias (64) | t2 bias (padded to 32)
+static_assert(NSTAGE_AR <= 8 * 16 * 64, "the AR pieces fit in the W2 area");
+
 // hidden unit of B slot j, lane half h, layer-2/head K step s
 __host__ __device__ constexpr int kperm(int s, int h, int j) {
     return 32 * (s >> 1) + 16 * (s & 1) + 8 * (j >> 2) + 4 * h + (j & 3);
 }
 
-// SAMPLE: the epilogue also draws each sample's action with the counter-RNG sampler
-// (d1_sample.h, the arithmetic of d1_sample) at step t = (t_dev ? *t_dev : 0) + t_add;
-// logits may then be null.
-template <bool SAMPLE>
+// Outputs of the autoregressive epilogue (null pointers are skipped; action, logp and value
+// are required)
+struct ArOut {
+    const uint16_t *bt;     // t1 bias [64] | t2 bias [25] (bf16)
+    int32_t *verb, *target;
+    float *verb_logits;     // [M, 8]
+    float *target_logits;   // [M, 25]: the drawn verb's row
+};
+
+// a register-array element chosen at run time without a run-time register index (which
+// would send the array to scratch): a select chain
+template <int K>
+__device__ __forceinline__ float sel(const float (&r)[K], int j) {
+    float v = r[0];
+#pragma unroll
+    for (int q = 1; q < K; q++) v = j == q ? r[q] : v;
+    return v;
+}
+__device__ __forceinline__ float bfr(float x) { return __uint_as_float(cvt2(x, 0.f) << 16); }   // bf16-rounded
+__device__ __forceinline__ float bhalf(u32x2 w, int i) {
+    return bf((uint16_t)((i < 2 ? w.x : w.y) >> (16 * (i & 1))));
+}
+
+// The autoregressive head after layer 2 (h2 in hf, B-fragment order). Head tiles: tile 0
+// (verb logits rows 0-7, value row 16) staged with W2, the two t1 tiles at pieces [0, 2048).
+// Lane half h draws for sample block h (sample m0 + 32h + lr): it gathers the block's eight
+// verb logits from its partner lane (l ^ 32), draws the verb with u0, and the partner learns
+// it back; each lane then forms z = tanh(bf16(ht + ev[verb])) for its 32 hidden units of both
+// blocks in the B-fragment order of the t2 tile (unit kperm(s, h, j) in step s, slot j), and
+// one K = 64 MFMA chain gives the drawn verb's 25 target logits, which the lane halves gather
+// as they did the verb logits and draw with u1. Rounding follows the bf16 torch forward:
+// every linear output is rounded once after its bias, ht + ev and tanh are rounded to bf16.
+__device__ __forceinline__ void ar_epilogue(const u32x4 *stage, const uint16_t *bl, const bf16x8 (&hf)[2][16],
+                                            int lane, int lr, int lh, int m0, int M, uint32_t key0, uint32_t key1,
+                                            uint32_t tstep, float *__restrict__ value, int64_t *__restrict__ actions,
+                                            float *__restrict__ logp, const ArOut &ar) {
+    floatx16 z0[2] = {}, z1[2] = {}, z2[2] = {};
+    {
+        const u32x4 *w0p = stage + 8 * 16 * 64 + lane, *w1p = stage + lane, *w2p = stage + 16 * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const bf16x8 f0 = as_bf(w0p[s * 64]), f1 = as_bf(w1p[s * 64]), f2 = as_bf(w2p[s * 64]);
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                z0[a] = mfma(f0, hf[a][s], z0[a]);
+                z1[a] = mfma(f1, hf[a][s], z1[a]);
+                z2[a] = mfma(f2, hf[a][s], z2[a]);
+            }
+        }
+    }
+    const uint16_t *b3l = bl + 512, *btl = bl + 544;
+    const uint32_t hm = 0u - (uint32_t)lh;
+    auto pick = [&](float if0, float if1) {
+        return __uint_as_float((__float_as_uint(if1) & hm) | (__float_as_uint(if0) & ~hm));
+    };
+    // verb logits 4lh..4lh+3 of block a in z0[a][0..3], the value (lane half 0) in z0[a][8]
+    float ov[2][4], val[2];
+    {
+        const u32x2 bw = *(const u32x2 *)(b3l + 4 * lh);
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) ov[a][i] = bfr(z0[a][i] + bhalf(bw, i));
+            val[a] = bfr(z0[a][8] + bf(b3l[16]));
+        }
+    }
+    float l8[NV];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float q = __shfl_xor(pick(ov[1][i], ov[0][i]), 32);
+        l8[i] = pick(ov[0][i], q);
+        l8[4 + i] = pick(q, ov[1][i]);
+    }
+    const int m = m0 + 32 * lh + lr;
+    uint32_t w0, w1;
+    d1s::philox_w01(0u, tstep, (uint32_t)m, 3u, key0, key1, w0, w1);
+    int v;
+    float lv;
+    d1s::cat_core([&](int j) { return l8[j]; }, NV, d1s::unit24(w0), v, lv);
+    const int vq = __shfl_xor(v, 32);
+    const int va[2] = {lh ? vq : v, lh ? v : vq};   // the drawn verbs of blocks 0 and 1 of sample row lr
+
+    // t2's B operand: z of this lane's hidden units for both blocks
+    bf16x8 hz[2][4];
+    const uint16_t *evl = (const uint16_t *)(stage + (PAE - PA1) / 8);
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int T = 0; T < 2; T++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {   // registers 4g..4g+3: units 32T + 8g + 4lh + 0..3
+                const int u0 = 32 * T + 8 * g + 4 * lh;
+                const u32x2 bw = *(const u32x2 *)(btl + u0);
+                const u32x2 ew = *(const u32x2 *)(evl + va[a] * TH + u0);
+                float zz[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float ht = bfr((T ? z2[a] : z1[a])[4 * g + i] + bhalf(bw, i));
+                    zz[i] = tanhf(bfr(ht + bhalf(ew, i)));
+                }
+                u32x4 w = __builtin_bit_cast(u32x4, hz[a][2 * T + (g >> 1)]);
+                w[2 * (g & 1)] = cvt2(zz[0], zz[1]);
+                w[2 * (g & 1) + 1] = cvt2(zz[2], zz[3]);
+                hz[a][2 * T + (g >> 1)] = as_bf(w);
+            }
+    floatx16 zt[2] = {};
+    {
+        const u32x4 *w3p = stage + 2 * 16 * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const bf16x8 f = as_bf(w3p[s * 64]);
+#pragma unroll
+            for (int a = 0; a < 2; a++) zt[a] = mfma(f, hz[a][s], zt[a]);
+        }
+    }
+    // target row 8g + 4lh + i of block a sits in register 4g + i; lane half h gathers block h's
+    float tl[NT];
+    {
+        const uint16_t *bt2 = btl + TH;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const u32x2 bw = *(const u32x2 *)(bt2 + 8 * g + 4 * lh);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float o0 = bfr(zt[0][4 * g + i] + bhalf(bw, i)), o1 = bfr(zt[1][4 * g + i] + bhalf(bw, i));
+                const float q = __shfl_xor(pick(o1, o0), 32);
+                if (8 * g + i < NT) tl[8 * g + i] = pick(o0, q);
+                if (8 * g + 4 + i < NT) tl[8 * g + 4 + i] = pick(q, o1);
+            }
+        }
+    }
+    int tg;
+    float lt;
+    d1s::cat_core([&](int j) { return tl[j]; }, NT, d1s::unit24(w1), tg, lt);
+    if (m < M) {
+        actions[m] = d1s::ar_action(v, tg);
+        logp[m] = lv + lt;
+        if (ar.verb) ar.verb[m] = v;
+        if (ar.target) ar.target[m] = tg;
+        if (ar.verb_logits) {
+            *(float4 *)(ar.verb_logits + (size_t)m * NV) = make_float4(l8[0], l8[1], l8[2], l8[3]);
+            *(float4 *)(ar.verb_logits + (size_t)m * NV + 4) = make_float4(l8[4], l8[5], l8[6], l8[7]);
+        }
+        if (ar.target_logits) {
+#pragma unroll
+            for (int j = 0; j < NT; j++) ar.target_logits[(size_t)m * NT + j] = tl[j];
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+        const int ma = m0 + 32 * a + lr;
+        if (ma < M && lh == 0) value[ma] = val[a];
+    }
+}
+
+// MODE 0: logits and value. MODE 1: the epilogue also draws each sample's action with the
+// counter-RNG sampler (d1_sample.h, the arithmetic of d1_sample) at step t = (t_dev ? *t_dev :
+// 0) + t_add; logits may then be null. MODE 2: the autoregressive head with its two-stage
+// sample (the arithmetic of d1_sample_ar).
+template <int MODE>
 __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs, int M, const uint16_t *__restrict__ wpk,
                                                 const uint16_t *__restrict__ b1, const uint16_t *__restrict__ b2,
                                                 const uint16_t *__restrict__ b3, float *__restrict__ logits,
                                                 float *__restrict__ value, uint32_t key0, uint32_t key1,
                                                 const uint32_t *__restrict__ t_dev, uint32_t t_add,
-                                                int64_t *__restrict__ actions, float *__restrict__ logp) {
-    __shared__ __align__(16) uint8_t lds[LDS_BYTES];
+                                                int64_t *__restrict__ actions, float *__restrict__ logp, ArOut ar) {
+    constexpr bool SAMPLE = MODE == 1, AR = MODE == 2;
+    __shared__ __align__(16) uint8_t lds[AR ? LDS_BYTES_AR : LDS_BYTES];
     const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
     u32x4 *stage = (u32x4 *)lds;                           // W1 double buffer, later W2 + head
     uint16_t *bl = (uint16_t *)(lds + LDS_W);              // [0,256) b1, [256,512) b2, [512,544) head bias
@@ -69,6 +242,7 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
     bl[t] = b1[t];
     bl[256 + t] = b2[t];
     if (t < 32) bl[512 + t] = t < NZ ? b3[t] : 0;
+    if (AR && t < TH + 32) bl[544 + t] = t < TH + NT ? ar.bt[t] : 0;
 
     floatx16 acc[2][8];
 #pragma unroll
@@ -279,8 +453,31 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
                 for (int a = 0; a < 2; a++) acc[a][b] = mfma(fw[b], hf[a][s], acc[a][b]);
         }
     }
-    to_frags(bl + 256);
+    if constexpr (AR) {
+        // The AR pieces go where W2 was: their loads are in flight while h2 is converted,
+        // and the LDS stores wait until every wave has read its last W2 fragment.
+        constexpr int RA = (NSTAGE_AR + 255) / 256;
+        u32x4 va[RA];
+#pragma unroll
+        for (int i = 0; i < RA; i++) {
+            const int piece = min(t + 256 * i, NSTAGE_AR - 1);
+            va[i] = *(const u32x4 *)(wpk + PA1 + (size_t)piece * 8);
+        }
+        to_frags(bl + 256);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < RA; i++)
+            if (t + 256 * i < NSTAGE_AR) stage[t + 256 * i] = va[i];
+        __syncthreads();
+    } else {
+        to_frags(bl + 256);
+    }
 
+    if constexpr (AR) {
+        ar_epilogue(stage, bl, hf, lane, lr, lh, m0, M, key0, key1, (t_dev ? *t_dev : 0u) + t_add, value, actions,
+                    logp, ar);
+        return;
+    }
     // ---- head: z[a] lane (lr, lh) register r = output 8(r/4) + 4lh + r%4 of sample 32a + lr
     floatx16 z[2] = {};
     {
@@ -384,9 +581,58 @@ __global__ __launch_bounds__(256) void k_policy_pack(const uint16_t *__restrict_
     }
 }
 
+// The autoregressive head's part of the packed buffer, [PA1, PAEND), same element rule:
+// the two t1 tiles (row 32T + r of t1, h2 unit kperm(s, h, j)), t2 (row r < 25, t1 unit
+// kperm(s, h, j) for s < 4, i.e. all 64), then ev copied as [8][64].
+__global__ __launch_bounds__(256) void k_policy_pack_ar(const uint16_t *__restrict__ t1w,
+                                                        const uint16_t *__restrict__ t2w,
+                                                        const uint16_t *__restrict__ ev, uint16_t *__restrict__ wpk) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < PAEND - PA1; e += gridDim.x * blockDim.x) {
+        const int j = e & 7, ln = (e >> 3) & 63, r = ln & 31, h = ln >> 5;
+        uint16_t v = 0;
+        if (e < PA2 - PA1) {
+            const int s = (e >> 9) & 15, tile = e >> 13;
+            v = t1w[(32 * tile + r) * (H + 16) + kperm(s, h, j)];
+        } else if (e < PAE - PA1) {
+            const int s = (e - (PA2 - PA1)) >> 9;
+            if (r < NT) v = t2w[r * TH + kperm(s, h, j)];
+        } else {
+            v = ev[e - (PAE - PA1)];
+        }
+        wpk[PA1 + e] = v;
+    }
+}
+
 }  // namespace d1t
 
 extern "C" int64_t d1_policy_packed_elems(void) { return d1t::PEND; }
+extern "C" int64_t d1_policy_ar_packed_elems(void) { return d1t::PAEND; }
+
+extern "C" int d1_policy_ar_pack(const void *w1, const void *w2, const void *w3, const void *t1w, const void *t2w,
+                                 const void *ev, void *wpk, void *stream) {
+    if (!w1 || !w2 || !w3 || !t1w || !t2w || !ev || !wpk || (uintptr_t)wpk % 16) return D1_E_ARG;
+    hipLaunchKernelGGL(d1t::k_policy_pack, dim3((d1t::PEND + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)w1, (const uint16_t *)w2, (const uint16_t *)w3, (uint16_t *)wpk);
+    hipLaunchKernelGGL(d1t::k_policy_pack_ar, dim3((d1t::PAEND - d1t::PA1 + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, (const uint16_t *)t1w, (const uint16_t *)t2w, (const uint16_t *)ev,
+                       (uint16_t *)wpk);
+    return (int)hipGetLastError();
+}
+
+extern "C" int d1_policy_fwd_sample_ar(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2,
+                                       const void *b3, const void *bt, uint64_t seed, const uint32_t *t_dev,
+                                       uint32_t t_add, float *value, int64_t *action, float *logp, int32_t *verb,
+                                       int32_t *target, float *verb_logits, float *target_logits, void *stream) {
+    if (M < 0 || (M > 0 && (!obs || !wpk || !b1 || !b2 || !b3 || !bt || !value || !action || !logp))) return D1_E_ARG;
+    if ((uintptr_t)obs % 8 || (uintptr_t)wpk % 16 || (uintptr_t)bt % 8 || (uintptr_t)verb_logits % 16)
+        return D1_E_ARG;
+    if (M == 0) return 0;
+    const d1t::ArOut ar{(const uint16_t *)bt, verb, target, verb_logits, target_logits};
+    hipLaunchKernelGGL(d1t::k_policy<2>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs, M,
+                       (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, nullptr,
+                       value, (uint32_t)seed, (uint32_t)(seed >> 32), t_dev, t_add, action, logp, ar);
+    return (int)hipGetLastError();
+}
 
 extern "C" int d1_policy_pack(const void *w1, const void *w2, const void *w3, void *wpk, void *stream) {
     if (!w1 || !w2 || !w3 || !wpk || (uintptr_t)wpk % 16) return D1_E_ARG;
@@ -400,9 +646,9 @@ extern "C" int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const v
     if (M < 0 || (M > 0 && (!obs || !wpk || !b1 || !b2 || !b3 || !logits || !value))) return D1_E_ARG;
     if ((uintptr_t)obs % 8 || (uintptr_t)wpk % 16 || (uintptr_t)logits % 16) return D1_E_ARG;
     if (M == 0) return 0;
-    hipLaunchKernelGGL(d1t::k_policy<false>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs,
+    hipLaunchKernelGGL(d1t::k_policy<0>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs,
                        M, (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, logits,
-                       value, 0u, 0u, nullptr, 0u, nullptr, nullptr);
+                       value, 0u, 0u, nullptr, 0u, nullptr, nullptr, d1t::ArOut{});
     return (int)hipGetLastError();
 }
 
@@ -412,8 +658,8 @@ extern "C" int d1_policy_fwd_sample(const uint8_t *obs, int M, const void *wpk, 
     if (M < 0 || (M > 0 && (!obs || !wpk || !b1 || !b2 || !b3 || !value || !actions || !logp))) return D1_E_ARG;
     if ((uintptr_t)obs % 8 || (uintptr_t)wpk % 16 || (uintptr_t)logits % 16) return D1_E_ARG;
     if (M == 0) return 0;
-    hipLaunchKernelGGL(d1t::k_policy<true>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs,
+    hipLaunchKernelGGL(d1t::k_policy<1>, dim3((M + d1t::BM - 1) / d1t::BM), dim3(256), 0, (hipStream_t)stream, obs,
                        M, (const uint16_t *)wpk, (const uint16_t *)b1, (const uint16_t *)b2, (const uint16_t *)b3, logits,
-                       value, (uint32_t)seed, (uint32_t)(seed >> 32), t_dev, t_add, actions, logp);
+                       value, (uint32_t)seed, (uint32_t)(seed >> 32), t_dev, t_add, actions, logp, d1t::ArOut{});
     return (int)hipGetLastError();
 }

@@ -70,24 +70,9 @@ __global__ __launch_bounds__(256) void k_gae(const float *__restrict__ reward, c
 
 // Two-stage (autoregressive) sample: verb ~ softmax(verb_logits[i]) with u0, then
 // target ~ softmax(target_logits[i][verb]) with u1, where u0/u1 = words 0/1 of
-// Philox4x32-10(ctr={0, t, i, 3}, key) scaled to [0,1) with 24 bits. logp = log p(verb) +
-// log p(target | verb). Env action: verb 0 MOVE / 1 ATTACK with target (dx, dy) =
-// (t%5-2, t/5-2) on a Chebyshev-1 ring -> direction d (N,E,S,W,NE,SE,SW,NW) -> d or 8+d,
-// other targets -> -1 (one WAIT turn); verb 2 WAIT(16), 3 REST(17), 4 DESCEND(18), 5-7 WAIT.
-__device__ __forceinline__ int cat_sample(const float *l, int k, float u, float &logp) {
-    float m = l[0];
-    for (int j = 1; j < k; j++) m = fmaxf(m, l[j]);
-    float s = 0.f;
-    for (int j = 0; j < k; j++) s += expf(l[j] - m);
-    float c = 0.f;
-    int a = k - 1;
-    for (int j = 0; j < k; j++) {
-        c += expf(l[j] - m) / s;
-        if (u < c) { a = j; break; }
-    }
-    logp = l[a] - m - logf(s);
-    return a;
-}
+// Philox4x32-10(ctr={0, t, i, 3}, key) scaled to [0,1) with 24 bits (d1_sample.h, shared
+// with the fused forward's epilogue); logp = log p(verb) + log p(target | verb); the env
+// action is d1s::ar_action(verb, target).
 __global__ __launch_bounds__(256) void k_sample_ar(const float *__restrict__ verb_logits, int nv, int ldv,
                                                    const float *__restrict__ target_logits, int nt, int ldt, int n,
                                                    uint32_t key0, uint32_t key1, uint32_t t, int32_t *__restrict__ verb,
@@ -95,30 +80,17 @@ __global__ __launch_bounds__(256) void k_sample_ar(const float *__restrict__ ver
                                                    float *__restrict__ logp) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    uint32_t c0 = 0u, c1 = t, c2 = (uint32_t)i, c3 = 3u, k0 = key0, k1 = key1;
-#pragma unroll
-    for (int r = 0; r < 10; r++) {
-        uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
-        uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
-        uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
-        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
-        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
-    }
-    float u0 = (float)(c0 >> 8) * (1.0f / 16777216.0f), u1 = (float)(c1 >> 8) * (1.0f / 16777216.0f);
+    uint32_t w0, w1;
+    d1s::philox_w01(0u, t, (uint32_t)i, 3u, key0, key1, w0, w1);
+    const float *vl = verb_logits + (size_t)i * ldv;
     float lv, lt;
-    int v = cat_sample(verb_logits + (size_t)i * ldv, nv, u0, lv);
-    int tg = cat_sample(target_logits + (size_t)i * ldt + (size_t)v * nt, nt, u1, lt);
-    int a = 16;
-    if (v <= 1) {
-        int dx = tg % 5 - 2, dy = tg / 5 - 2, d = -1;
-        if (dx == 0 && dy == -1) d = 0; else if (dx == 1 && dy == 0) d = 1; else if (dx == 0 && dy == 1) d = 2;
-        else if (dx == -1 && dy == 0) d = 3; else if (dx == 1 && dy == -1) d = 4; else if (dx == 1 && dy == 1) d = 5;
-        else if (dx == -1 && dy == 1) d = 6; else if (dx == -1 && dy == -1) d = 7;
-        a = d < 0 ? -1 : d + 8 * v;
-    } else if (v <= 4) a = 14 + v;
+    int v, tg;
+    d1s::cat_core([&](int j) { return vl[j]; }, nv, d1s::unit24(w0), v, lv);
+    const float *tl = target_logits + (size_t)i * ldt + (size_t)v * nt;
+    d1s::cat_core([&](int j) { return tl[j]; }, nt, d1s::unit24(w1), tg, lt);
     if (verb) verb[i] = v;
     if (target) target[i] = tg;
-    if (action) action[i] = a;
+    if (action) action[i] = d1s::ar_action(v, tg);
     if (logp) logp[i] = lv + lt;
 }
 

@@ -220,6 +220,71 @@ class ARPolicy(nn.Module):
         targets = self.t2(z)                                                             # [B, 8, 25]
         return self.verb(h).float(), targets.float(), self.value(h).float().squeeze(-1)
 
+    def packed(self, refresh=False):
+        """(packed weights, b1, b2, b3, bt) for policy_fwd_sample_ar (bf16 parameters only),
+        rebuilt when a parameter's storage or version counter changes (as Policy.packed).
+        The head holds the verb logits in rows 0-7 and the value in row 16; ev, the verb
+        embeddings through t1's embedding columns, is computed here by the same bf16 linear
+        as forward() computes it."""
+        params = (self.l1.weight, self.l2.weight, self.verb.weight, self.value.weight, self.embedding,
+                  self.t1.weight, self.t2.weight, self.l1.bias, self.l2.bias, self.verb.bias, self.value.bias,
+                  self.t1.bias, self.t2.bias)
+        if any(q.dtype != torch.bfloat16 or not q.is_cuda for q in params):
+            raise ValueError('the fused AR forward takes a CUDA model in bfloat16')
+        key = tuple((q.data_ptr(), q._version) for q in params)
+        if refresh or getattr(self, '_packed_key', None) != key:
+            with torch.no_grad():
+                dev, width = self.l1.weight.device, self.l2.out_features
+                w3 = torch.zeros((N_ACTIONS + 1, width), dtype=torch.bfloat16, device=dev)
+                w3[:N_VERBS] = self.verb.weight
+                w3[N_ACTIONS] = self.value.weight[0]
+                b3 = torch.zeros(N_ACTIONS + 1, dtype=torch.bfloat16, device=dev)
+                b3[:N_VERBS] = self.verb.bias
+                b3[N_ACTIONS] = self.value.bias[0]
+                t1w = self.t1.weight.detach()
+                ev = torch.nn.functional.linear(self.embedding.detach(), t1w[:, width:]).contiguous()
+                bt = torch.cat([self.t1.bias.detach(), self.t2.bias.detach()]).contiguous()
+                L = _lib.load()
+                wpk = torch.empty(L.d1_policy_ar_packed_elems(), dtype=torch.bfloat16, device=dev)
+                args = [self.l1.weight.detach().contiguous(), self.l2.weight.detach().contiguous(), w3,
+                        t1w.contiguous(), self.t2.weight.detach().contiguous(), ev]
+                _lib.check(L.d1_policy_ar_pack(*(a.data_ptr() for a in args), wpk.data_ptr(),
+                                               torch.cuda.current_stream(dev).cuda_stream), 'd1_policy_ar_pack')
+                self._packed_val = (wpk, self.l1.bias.detach().contiguous(), self.l2.bias.detach().contiguous(),
+                                    b3, bt)
+                self._packed_key = key
+        return self._packed_val
+
+
+def policy_fwd_sample_ar(obs_u8, packed, seed, t, action, logp, value, t_dev=None, verb=None, target=None,
+                         verb_logits=None, target_logits=None):
+    """ARPolicy's forward and its two-stage counter-RNG sample in one kernel
+    (d1_policy_fwd_sample_ar) on uint8 obs [B, 1800]: the verb, target, env action and
+    log-probability sample_ar() would draw from the same logits at step t (+ t_dev[0] when
+    given), without the [B, 8, 25] target logits (only the drawn verb's row is formed)."""
+    obs_u8 = obs_u8.reshape(obs_u8.shape[0], OBS).contiguous()
+    n = obs_u8.shape[0]
+    assert obs_u8.dtype == torch.uint8
+    wpk, b1, b2, b3, bt = packed
+    assert action.dtype == torch.int64 and logp.dtype == torch.float32 and value.dtype == torch.float32
+    assert action.numel() == n and logp.numel() == n and value.numel() == n
+    for x, dt, width in ((verb, torch.int32, 1), (target, torch.int32, 1), (verb_logits, torch.float32, N_VERBS),
+                         (target_logits, torch.float32, N_TARGETS)):
+        if x is not None and (x.dtype != dt or x.numel() != n * width or not x.is_contiguous()):
+            raise ValueError('optional outputs: contiguous int32 verb/target [B], fp32 verb_logits [B, 8] and '
+                             'target_logits [B, 25]')
+    if t_dev is not None and t_dev.dtype != torch.int32:
+        raise ValueError('t_dev must be an int32 device tensor')
+    ptr = lambda x: None if x is None else x.data_ptr()
+    L = _lib.load()
+    _lib.check(L.d1_policy_fwd_sample_ar(obs_u8.data_ptr(), n, wpk.data_ptr(), b1.data_ptr(), b2.data_ptr(),
+                                         b3.data_ptr(), bt.data_ptr(), seed, ptr(t_dev), t & 0xFFFFFFFF,
+                                         value.data_ptr(), action.data_ptr(), logp.data_ptr(), ptr(verb),
+                                         ptr(target), ptr(verb_logits), ptr(target_logits),
+                                         torch.cuda.current_stream(obs_u8.device).cuda_stream),
+               'd1_policy_fwd_sample_ar')
+    return action, logp, value
+
 
 class ARDistribution:
     """p(verb) p(target | verb) with the factorised log-prob and entropy

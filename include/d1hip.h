@@ -190,6 +190,28 @@ int d1_policy_fwd(const uint8_t *obs, int M, const void *wpk, const void *b1, co
 int d1_policy_fwd_sample(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
                          uint64_t seed, const uint32_t *t_dev, uint32_t t_add, float *logits, float *value,
                          int64_t *actions, float *logp, void *stream);
+/* The autoregressive verb x target policy (BASELINE C5; the reference's two-stage head,
+ * gpu-d1/branches/autoregressive-actions-v1/scripts/tactical_models.py:8-48, at 8 verbs x 25
+ * targets with a 16-wide verb embedding and a 64-unit tanh target MLP) as one kernel: the
+ * trunk above, a 17-row head holding the 8 verb logits (rows 0-7, rows 8-15 zero) and the
+ * value (row 16), then verb ~ softmax(verb logits) and target ~ softmax(t2 . tanh(t1[:, :256]
+ * . h2 + t1 bias + ev[verb]) + t2 bias) with the two-stage counter-RNG draw of d1_sample_ar
+ * (bit-identical on the same logits), at step t = (t_dev ? *t_dev : 0) + t_add. Writes
+ * action (d1_sample_ar's env action), logp = log p(verb) + log p(target | verb) and value;
+ * verb, target, verb_logits [M, 8] (16-byte aligned) and the drawn verb's target_logits
+ * [M, 25] when not null. Pack once per weight update with d1_policy_ar_pack(w1, w2, w3 [17,256]
+ * (verb rows 0-7, value row 16), t1 [64, 272], t2 [25, 64], ev [8, 64] = t1[:, 256:] .
+ * embedding^T (bf16), wpk of d1_policy_ar_packed_elems() bf16); bt = t1 bias [64] then t2
+ * bias [25] (bf16, 8-byte aligned). Replaces the policy forward + the two-stage sample of the
+ * reference's rollout (tactical_models.py:39-48 and run_ring_ablations.py:347-351 of that
+ * branch). */
+int64_t d1_policy_ar_packed_elems(void);
+int d1_policy_ar_pack(const void *w1, const void *w2, const void *w3, const void *t1w, const void *t2w, const void *ev,
+                      void *wpk, void *stream);
+int d1_policy_fwd_sample_ar(const uint8_t *obs, int M, const void *wpk, const void *b1, const void *b2, const void *b3,
+                            const void *bt, uint64_t seed, const uint32_t *t_dev, uint32_t t_add, float *value,
+                            int64_t *action, float *logp, int32_t *verb, int32_t *target, float *verb_logits,
+                            float *target_logits, void *stream);
 
 /* D4 camera augmentation of the uint8 observation (the reference's EpisodeSymmetry,
  * gpu-d1/branches/autoregressive-actions-v1/scripts/symmetry.py:10-70, restated for the

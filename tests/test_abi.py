@@ -20,7 +20,8 @@ def test_header_declares_the_abi():
                                          'd1_ppo_step_static',
                                          'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
                                          'd1_sample_ar', 'd1_los_table', 'd1_distance_rows', 'd1_policy_packed_elems',
-                                         'd1_policy_pack', 'd1_policy_fwd', 'd1_policy_fwd_sample'])
+                                         'd1_policy_pack', 'd1_policy_fwd', 'd1_policy_fwd_sample',
+                                         'd1_policy_ar_packed_elems', 'd1_policy_ar_pack', 'd1_policy_fwd_sample_ar'])
     # the reference's learn_* exports (gpu-d1/branches/d1-stairs-v2/src/learn.cu:913-946)
     assert declared_symbols('d1learn.h', 'learn_') == sorted(
         ['learn_turn_cost', 'learn_return_gamma', 'learn_state_bytes', 'learn_obs_size', 'learn_action_size',
@@ -132,6 +133,15 @@ def test_policy_fwd_validation_without_gpu(pkg):
     assert L.d1_policy_fwd(fake + 4, 4, fake, fake, fake, fake, fake, fake, None) == -1   # obs not 8-byte aligned
     assert L.d1_policy_fwd(fake, 4, fake + 8, fake, fake, fake, fake, fake, None) == -1   # packed weights not 16-byte aligned
     assert L.d1_policy_fwd(fake, 4, fake, fake, fake, fake, fake + 4, fake, None) == -1   # logits not 16-byte aligned
+    # the autoregressive head's region after it: two t1 tiles [2][16][64][8], t2 [4][64][8], ev [8][64]
+    assert L.d1_policy_ar_packed_elems() == L.d1_policy_packed_elems() + 2 * 16 * 512 + 4 * 512 + 8 * 64
+    assert L.d1_policy_ar_pack(None, None, None, None, None, None, None, None) == -1
+    args = [fake, 4, fake, fake, fake, fake, fake, 0, None, 0, fake, fake, fake, None, None, None, None, None]
+    assert L.d1_policy_fwd_sample_ar(*args[:1], 0, *args[2:]) == 0                       # empty batch
+    for k, bad in ((0, fake + 4), (2, fake + 8), (6, fake + 2), (15, fake + 4), (10, None), (11, None)):
+        a = list(args)
+        a[k] = bad                                                                     # misaligned or missing
+        assert L.d1_policy_fwd_sample_ar(*a) == -1, k
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):

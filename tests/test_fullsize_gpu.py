@@ -71,21 +71,22 @@ def test_c5_full_size_slice(pkg):
 
 def test_c5_ar_head_workload(pkg):
     """C5's bench workload (bench.py --mode stress): the stress layout driven by the
-    autoregressive verb x target head through its HIP sampler, whose actions include waits,
-    REST, stairs and unreachable targets (-1) besides moves and attacks. 8,192 worlds x 96
-    steps; the first 2,048 are replayed on the host with the same actions (hash and out every
-    step, observations every 16th)."""
+    autoregressive verb x target policy and its two-stage draw fused in one kernel
+    (d1_policy_fwd_sample_ar), whose actions include waits, REST, stairs and unreachable
+    targets (-1) besides moves and attacks. 8,192 worlds x 96 steps; the first 2,048 are
+    replayed on the host with the same actions (hash and out every step, observations every
+    16th)."""
     P = importlib.import_module('dcss-auto_amd.policy')
     cfg = pkg.stress_config()
     n, n_cpu, steps = 8192, 2048, 96
     gpu = pkg.Env(n, cfg, seed=3)
     cpu = O.OracleEnv(n_cpu, cfg, seed=3, threads=16)
     model = P.ARPolicy(seed=0).cuda().to(torch.bfloat16)
+    a = torch.empty(n, dtype=torch.int64, device='cuda')
+    logp, value = torch.empty(n, device='cuda'), torch.empty(n, device='cuda')
     seen, dones = set(), 0
     for k in range(steps):
-        with torch.no_grad():
-            vl, tl, _ = model(gpu.obs)
-        _, _, a, _ = P.sample_ar(vl, tl, 11, k)
+        P.policy_fwd_sample_ar(gpu.obs, model.packed(), 11, k, a, logp, value)
         an = a.cpu().numpy()
         seen.update(np.unique(an[:n_cpu]).tolist())
         gpu.step(a)
