@@ -328,6 +328,14 @@ struct Ctx {
     // this lane's monster (lane < count)
     int mpos, mhp, menergy, mawake, mkind;
     int mlay;    // absolute BFS layer of the monster's cell (FAR when not known)
+    // Stuck cache (kernels whose distance field depends on the player cell alone set
+    // stuck_cache): mrad > 0 records that this lane's monster found no move with the player
+    // on the current cell, and that the search behind that answer read no cell farther than
+    // mrad (Chebyshev) from the monster. The answer stands while the player stays and no cell
+    // within mrad changes occupancy (a move or a death there, or the monster's own move,
+    // clears it), so the next act draws its rotation and waits without searching.
+    int mrad = 0;
+    bool stuck_cache = false;
     int lastl;   // last layer the field holds: a reached cell next to an unreached one is on it
     int lane;
     // distance-field memo in the state row (crowded layouts): its address, the player cell the
@@ -613,8 +621,9 @@ __device__ __forceinline__ int next_layer(const Cell &c, int hlay, int hm, int l
     if (!c.reached) return RQ_FAR;
     return hlay < RQ_FAR ? hlay + step3(c.m3, hm) : lastl;
 }
-// Returns the first step's direction from p (-1: none).
-__device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, int ply, int mp, int plag) {
+// Returns the first step's direction from p (-1: none); with -1, rad is the largest Chebyshev
+// distance from p of a cell the search read (its queued cells' neighbours).
+__device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, int ply, int mp, int plag, int &rad) {
     Smem *sm = x.sm;
     const int hoff = x.lane >> 3, dir = x.lane & 7, dx = ddx(dir), dy = ddy(dir);
     const int lastl = imin(x.lastl, RQ_FAR - 1);
@@ -668,11 +677,14 @@ __device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, in
         const uint64_t lm = ballot(c.walk && nlay < plag);
         if (lm) result = lane_val(h == 0 ? dir : hf, __ffsll((unsigned long long)lm) - 1);
     }
+    int qd = 0;
     if (x.lane < len) {
         const uint32_t qw = sm->rq[x.lane];
         const int qx = (int)(qw & 127u), qy = (int)((qw >> 7) & 127u);
         atomicAnd(&sm->front[qy * RW + (qx >> 5)], ~(1u << (qx & 31)));
+        qd = imax(iabs(qx - px), iabs(qy - py));
     }
+    if (result < 0 && x.stuck_cache) rad = wave_max(qd) + 1;
     __syncthreads();
     return result;
 }
@@ -696,7 +708,8 @@ __device__ __forceinline__ int repair_search(Ctx &x, int px, int py, int plx, in
 // plag - 1 next to a possible offset 0 is the first place where a lower cell can appear.
 // Returns true when rings 1..D+1 hold no such cell; false (run the search) when one may
 // exist or the rings reach the window edge.
-__device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, int plx, int ply, int mp) {
+// On true, ring is the last ring grown: every cell the search would read lies within it.
+__device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, int plx, int ply, int mp, int &ring) {
     const Smem *sm = x.sm;
     const int y = py - 31 + x.lane;
     // window bit b is column px-15+b; with a zero word prepended to the row, that is bit
@@ -732,9 +745,11 @@ __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, i
     };
     uint32_t p0 = x.lane == 31 ? 1u << 15 : 0u, p1 = 0, g = 0, seen = p0;
     int count = 1;
+    ring = 0;
     for (bool last = false;; ) {
         const uint32_t d0 = dil(p0), d1 = dil(p1), dg = dil(g);
         const uint32_t n = (d0 | d1 | dg) & walk & ~seen;
+        ring++;
         if (ballot((n & c2 & d0) != 0)) return false;   // possibly lower than p
         const uint64_t rows = ballot(n != 0);
         if (!rows) return true;                         // the component ends
@@ -753,7 +768,7 @@ __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, i
 // replacement, then a bounded 24-node BFS detour when stuck. p is a reached cell at
 // absolute layer plag (every mover is reached before the field stops growing); the chosen
 // cell's layer goes to qlag.
-__device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
+__device__ __forceinline__ int choose_move(Ctx &x, int id, int p, int plag, int &qlag) {
     int rotation = x.g.r(4);
     const Smem *sm = x.sm;
     const int px = p % W, py = p / W, plx = x.player % W, ply = x.player / W;
@@ -777,9 +792,18 @@ __device__ __forceinline__ int choose_move(Ctx &x, int p, int plag, int &qlag) {
         return best;
     }
     // With no walkable neighbour the search would queue nothing after p and find nothing.
-    if (!x.c->repair || !ballot(c.walk) || detour_ruled_out(x, px, py, plx, ply, mp)) return -1;
-    const int fd = repair_search(x, px, py, plx, ply, mp, imin(plag, RQ_FAR - 1));
-    if (fd < 0) return -1;
+    if (!x.c->repair || !ballot(c.walk)) return -1;
+    if (x.stuck_cache && lane_val(x.mrad, id) > 0) return -1;   // still stuck
+    int rad = 0;
+    if (detour_ruled_out(x, px, py, plx, ply, mp, rad)) {
+        if (x.stuck_cache && x.lane == id) x.mrad = rad;
+        return -1;
+    }
+    const int fd = repair_search(x, px, py, plx, ply, mp, imin(plag, RQ_FAR - 1), rad);
+    if (fd < 0) {
+        if (x.stuck_cache && x.lane == id) x.mrad = rad;
+        return -1;
+    }
     const int sx = px + ddx(fd), sy = py + ddy(fd);
     const Cell sc = cell_at(sm, sx, sy, plx, ply);   // a reached neighbour of p
     qlag = plag + step3(sc.m3, mp);
@@ -866,6 +890,10 @@ __device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
     if (has1) { row_st(sm->reach, 64 + lane, r1); row_st(sm->lay0, 64 + lane, a1); row_st(sm->lay1, 64 + lane, b1); }
     __syncthreads();
 }
+// Cells a and b changed occupancy: stuck answers whose search read either are dropped.
+__device__ __forceinline__ void stuck_touch(Ctx &x, int a, int b) {
+    if (x.mrad > 0 && (cheb(x.mpos, a) <= x.mrad || cheb(x.mpos, b) <= x.mrad)) x.mrad = 0;
+}
 // gpu-d1/src/sim.h:254-269
 // The mover's absolute layer follows it (the cell it steps to is a reached neighbour).
 __device__ __forceinline__ void act(Ctx &x, int id) {
@@ -873,13 +901,14 @@ __device__ __forceinline__ void act(Ctx &x, int id) {
     int p = lane_val(x.mpos, id);
     if (cheb(p, x.player) == 1) { attack(x, lane_val(x.mkind, id)); return; }
     int qlag = FAR;
-    int q = choose_move(x, p, lane_val(x.mlay, id), qlag);
+    int q = choose_move(x, id, p, lane_val(x.mlay, id), qlag);
     if (q >= 0) {
         if (x.lane == 0) {   // occupancy follows the monster (one lane, then a wave-wide wait)
             uint32_t *occ = x.sm->occ;
             occ[(p / W) * RW + ((p % W) >> 5)] &= ~(1u << ((p % W) & 31));
             occ[(q / W) * RW + ((q % W) >> 5)] |= 1u << ((q % W) & 31);
         }
+        if (x.stuck_cache) stuck_touch(x, p, q);   // the mover's own entry too (p is its cell)
         __syncthreads();
         if (x.lane == id) { x.mpos = q; x.mlay = qlag; }
     }

@@ -53,8 +53,9 @@ __host__ __device__ constexpr int off_floor(int m) { return off_viewed(m) + ROWS
 __host__ __device__ constexpr int off_cells(int m) { return off_floor(m) + ROWS_WORDS * 4; }
 // Layouts with more than 8 monsters also keep the distance-field memo: dword 0 the player
 // cell it was computed for (-1: none), dword 1 its last layer, dwords 2-33 the monsters'
-// absolute layers (int16 each, 32767 = unknown), then the reach, lay0 and lay1 bitmaps.
-constexpr int FC_HEAD = 34, FC_DWORDS = FC_HEAD + 3 * ROWS_WORDS;
+// absolute layers (int16 each, 32767 = unknown), dwords 34-49 the monsters' stuck-cache
+// radii (uint8 each, 0 = none; Ctx::mrad), then the reach, lay0 and lay1 bitmaps.
+constexpr int FC_RAD = 34, FC_HEAD = 50, FC_DWORDS = FC_HEAD + 3 * ROWS_WORDS;
 __host__ __device__ constexpr bool has_fcache(int m) { return m > 8; }
 __host__ __device__ constexpr int off_fcache(int m) { return off_cells(m) + ROWS_WORDS * 4; }
 __host__ __device__ constexpr int state_bytes(int m) {
@@ -125,6 +126,7 @@ __device__ __forceinline__ void reset(Ctx &x, const uint32_t *cells_g) {
     reveal(x);
     x.ftag = -1;   // a new player cell and new monster cells: the memo no longer applies
     x.fld = -1;    // and the reach bitmap held the stairs' eligible cells
+    x.mrad = 0;    // nor does any stuck answer
 }
 
 // ---------------------------------------------------------------- distance-field memo
@@ -183,6 +185,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
                     int nh = (int16_t)(lane_val(x.mhp, id) - dmg);
                     if (nh <= 0) {
                         if (x.lane == id) { x.mhp = 0; x.menergy = -30000; }
+                        if (x.stuck_cache) stuck_touch(x, p, p);   // its cell frees
                         occ_set(x, p, false);
                         x.killed++;
                         milli += c->kill_milli;
@@ -191,6 +194,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
             } else {
                 x.player = p;
                 moved = true;
+                x.mrad = 0;   // a new distance field: no stuck answer stands
             }
         }
     }
@@ -405,7 +409,10 @@ __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
     if (has_fcache(max_m)) {   // memo head: its player cell, last layer, the monsters' layers
         uint32_t *fc = (uint32_t *)(row + off_fcache(max_m));
         if (x.lane == 0) { fc[0] = (uint32_t)x.ftag; fc[1] = (uint32_t)x.lastl; }
-        if (x.lane < max_m) ((int16_t *)(fc + 2))[x.lane] = (int16_t)imin(x.mlay, 32767);
+        if (x.lane < max_m) {
+            ((int16_t *)(fc + 2))[x.lane] = (int16_t)imin(x.mlay, 32767);
+            ((uint8_t *)(fc + FC_RAD))[x.lane] = (uint8_t)imin(x.mrad, 255);
+        }
     }
 }
 
@@ -514,8 +521,11 @@ __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
         const uint32_t pair = (uint32_t)__shfl((int)pf.fh, 2 + (x.lane >> 1));
         const int ml = (int16_t)(x.lane & 1 ? pair >> 16 : pair & 0xFFFFu);
         x.mlay = ml >= 32767 ? FAR : ml;
+        const uint32_t quad = (uint32_t)__shfl((int)pf.fh, FC_RAD + (x.lane >> 2));
+        x.mrad = x.lane < max_m ? (int)((quad >> (8 * (x.lane & 3))) & 255u) : 0;
     } else {
         x.ftag = -1;
+        x.mrad = 0;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -592,6 +602,7 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
     Ctx x;
     x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
     x.view_lds = CROWD;   // the crowded build keeps the player view in LDS
+    x.stuck_cache = CROWD;   // and a complete distance field that depends on the player cell alone
     Pre pf;
     prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
     for (int env = first; env < last; env++) {

@@ -30,9 +30,10 @@ from . import policy as P
 from . import ppo as ppo_mod
 
 # Checkpoint layout version: 2 added the trainer-settings record and grew crowded env state
-# rows (more than 8 monsters) by the 2,656-byte distance-field memo; version-1 files carry no
-# 'format' key.
-CHECKPOINT_FORMAT = 2
+# rows (more than 8 monsters) by the 2,656-byte distance-field memo; 3 added the monsters'
+# stuck-cache radii to that memo (rows of 40 monsters 5,632 -> 5,696 bytes); version-1 files
+# carry no 'format' key.
+CHECKPOINT_FORMAT = 3
 
 
 class Trainer:
@@ -174,8 +175,8 @@ class Trainer:
         F = self.ppo.flat
         if sd.get('format') != CHECKPOINT_FORMAT:
             raise ValueError(f"checkpoint format {sd.get('format', 1)} is not this trainer's ({CHECKPOINT_FORMAT}): "
-                             'it was written by an older version (no settings record; env state rows of '
-                             'crowded layouts without the distance-field memo) and cannot be resumed')
+                             'it was written by an older version (no settings record, or env state rows of '
+                             'crowded layouts in an older memo layout) and cannot be resumed')
         saved = sd.get('hparams')
         if saved != self.hparams:
             diff = sorted(k for k in set(self.hparams) | set(saved or {})

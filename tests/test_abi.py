@@ -64,7 +64,7 @@ def test_library_exports_declared_symbols(pkg):
         assert hasattr(lib, name), name
     assert lib.d1_obs_bytes() == 1800 and lib.d1_action_size() == 19 and lib.d1_out_size() == 8
     assert lib.d1_config_bytes() == C.sizeof(pkg.D1Config)
-    assert lib.d1_state_bytes(8) == 2688 and lib.d1_state_bytes(40) == 5632   # 40: + the distance-field memo
+    assert lib.d1_state_bytes(8) == 2688 and lib.d1_state_bytes(40) == 5696   # 40: + the distance-field memo
     assert lib.d1_state_bytes(0) < 0 and lib.d1_state_bytes(65) < 0
 
 
