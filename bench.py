@@ -254,6 +254,32 @@ def roofline(kernel, achieved, launch_ms, step_bytes, traffic, launches):
     return r
 
 
+def stress_counters(args, envs=262144, horizon=256, warmup=4):
+    """The C5 stress workload of stress_bench (same worlds, policy, seeds and steps), after a
+    256 MiB device copy that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE, untimed: the
+    k_step_crowd dispatches warmup+1 .. warmup+horizon are the bench's timed launches."""
+    import torch
+    pkg = importlib.import_module('dcss-auto_amd')
+    P = importlib.import_module('dcss-auto_amd.policy')
+    dev = torch.device('cuda:0')
+    src = torch.ones(64 << 20, dtype=torch.int32, device=dev)   # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    env = pkg.Env(envs, pkg.stress_config(), seed=3, hash=False)
+    model = P.ARPolicy(seed=0).to(dev).to(torch.bfloat16)
+    packed = model.packed()
+    actions = torch.zeros(envs, dtype=torch.int64, device=dev)
+    logp, value = torch.empty(envs, device=dev), torch.empty(envs, device=dev)
+    obs = env.obs.view(envs, -1)
+    for t in range(warmup + horizon):
+        env.step(actions)
+        P.policy_fwd_sample_ar(obs, packed, 11, t, actions, logp, value)
+    torch.cuda.synchronize()
+    return {'mode': 'stress-counters', 'copy_bytes': src.numel() * 4, 'env_steps': warmup + horizon, 'envs': envs,
+            'timed_dispatches': [warmup + 1, warmup + horizon]}
+
+
 def stress_bench(args, envs=262144, horizon=256, warmup=4):
     """C5: 262,144 generated-level worlds with 40 monsters (HP U[40,60], half awake at
     spawn), the bf16 trunk with the autoregressive verb(8) x target(25) head and its
@@ -378,9 +404,11 @@ def main():
     ap.add_argument('--envs', type=int, default=65536)
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'train', 'panel', 'wait', 'stress', 'learn'],
+    ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'train', 'panel', 'wait', 'stress',
+                                       'stress-counters', 'learn'],
                     default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
+                         'stress-counters: the same calibration, then the C5 stress workload untimed; '
                          'ppo: C4, GAE + 4-epoch PPO update over a T x envs rollout buffer; '
                          'train: rollout + update iterations of the training loop')
     ap.add_argument('--horizon', type=int, default=128, help='T of the PPO rollout buffer')
@@ -399,6 +427,9 @@ def main():
         return
     if args.mode == 'stress':
         print(json.dumps(stress_bench(args)), flush=True)
+        return
+    if args.mode == 'stress-counters':
+        print(json.dumps(stress_counters(args)), flush=True)
         return
     if args.mode == 'learn':
         print(json.dumps(learn_bench(args)), flush=True)

@@ -224,6 +224,17 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
         }
         // a ballot ends the loop when no monster can act (most turns), before any reduction
         while (x.hp > 0 && ballot(mine && x.menergy >= 80)) {
+            // The lane id made opaque per act: the lane-derived addresses and masks of the
+            // monster rules are then recomputed in each act instead of being held from the
+            // world's start through the whole loop, where the crowded build (80 VGPRs at 6
+            // waves per SIMD) spilled them to scratch and both builds spilled their lane masks
+            // from SGPRs to VGPR lanes (k_step_crowd 2.30 -> 2.16 ms at C5, k_step 0.158 ->
+            // 0.152 ms at C3).
+            {
+                int l = lane_id();
+                asm volatile("" : "+v"(l));
+                x.lane = l;
+            }
             const int key = wave_max(mine && x.menergy >= 80 ? x.menergy * 128 + 127 - x.lane : -1);
             int id = 127 - (key & 127);
             act(x, id);
@@ -603,8 +614,13 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
     x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
     x.view_lds = CROWD;   // the crowded build keeps the player view in LDS
     x.stuck_cache = CROWD;   // and a complete distance field that depends on the player cell alone
+    // The <= 8 monster build fetches each next world while the current one stores its state
+    // and observation. A crowded world steps for tens of microseconds, so its load latency
+    // is small beside it and other waves hide it, while the prefetched row held across the
+    // store and the observation went to scratch (about 7 KB of spill traffic per world):
+    // the crowded build loads each world when it starts it.
     Pre pf;
-    prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
+    if (!CROWD) prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
     for (int env = first; env < last; env++) {
         // Opaque per world: otherwise every lane-derived constant of the world step is
         // hoisted out of this loop and kept live across it.
@@ -612,11 +628,12 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
         asm volatile("" : "+v"(lane));
         x.lane = lane;
         uint8_t *row = state + (size_t)env * row_bytes;
+        if (CROWD) prefetch_world(pf, row, max_m, actions, active, env, x.lane);
         const int on = __builtin_amdgcn_readfirstlane(pf.on);
         const int64_t a = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(pf.act >> 32)) << 32 |
                                     (uint32_t)__builtin_amdgcn_readfirstlane((int)pf.act));
         if (!on) {   // an inactive env keeps its state and all its output rows
-            if (env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
+            if (!CROWD && env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
             continue;
         }
         unpack_world<RM>(x, pf, max_m);
@@ -627,7 +644,7 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
         transition(x, action, o8, cg);
         x.t++;
         // the next world's loads overlap this world's stores, observation and digest
-        if (env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
+        if (!CROWD && env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
         store_world(x, row, max_m);
         if (out && x.lane == 0) {
             float4 *o4 = (float4 *)(out + (size_t)env * D1_OUT);
