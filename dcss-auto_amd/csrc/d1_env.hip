@@ -614,13 +614,13 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
     x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
     x.view_lds = CROWD;   // the crowded build keeps the player view in LDS
     x.stuck_cache = CROWD;   // and a complete distance field that depends on the player cell alone
-    // The <= 8 monster build fetches each next world while the current one stores its state
-    // and observation. A crowded world steps for tens of microseconds, so its load latency
-    // is small beside it and other waves hide it, while the prefetched row held across the
-    // store and the observation went to scratch (about 7 KB of spill traffic per world):
-    // the crowded build loads each world when it starts it.
+    // Each world is loaded when the wave starts it. Fetching the next world's row while the
+    // current one stores its state and observation held 12 more registers across those
+    // phases: at 4 waves per SIMD it paid (0.176 -> 0.171 ms at C3), but with the lane
+    // masks no longer held through the monster loop both builds run more waves per SIMD
+    // without it, whose latency hiding does more (C3 k_step 0.152 -> 0.140 ms at 5 waves;
+    // in the crowded build the held row had gone to scratch, about 7 KB of traffic a world).
     Pre pf;
-    if (!CROWD) prefetch_world(pf, state + (size_t)first * row_bytes, max_m, actions, active, first, x.lane);
     for (int env = first; env < last; env++) {
         // Opaque per world: otherwise every lane-derived constant of the world step is
         // hoisted out of this loop and kept live across it.
@@ -628,14 +628,11 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
         asm volatile("" : "+v"(lane));
         x.lane = lane;
         uint8_t *row = state + (size_t)env * row_bytes;
-        if (CROWD) prefetch_world(pf, row, max_m, actions, active, env, x.lane);
+        prefetch_world(pf, row, max_m, actions, active, env, x.lane);
         const int on = __builtin_amdgcn_readfirstlane(pf.on);
         const int64_t a = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(pf.act >> 32)) << 32 |
                                     (uint32_t)__builtin_amdgcn_readfirstlane((int)pf.act));
-        if (!on) {   // an inactive env keeps its state and all its output rows
-            if (!CROWD && env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
-            continue;
-        }
+        if (!on) continue;   // an inactive env keeps its state and all its output rows
         unpack_world<RM>(x, pf, max_m);
         x.fcache = has_fcache(max_m) ? (uint32_t *)(row + off_fcache(max_m)) : nullptr;
         const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
@@ -643,8 +640,6 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
         float o8[8];
         transition(x, action, o8, cg);
         x.t++;
-        // the next world's loads overlap this world's stores, observation and digest
-        if (!CROWD && env + 1 < last) prefetch_world(pf, row + row_bytes, max_m, actions, active, env + 1, x.lane);
         store_world(x, row, max_m);
         if (out && x.lane == 0) {
             float4 *o4 = (float4 *)(out + (size_t)env * D1_OUT);
@@ -669,7 +664,7 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
 // (190 -> 104 spilled to VGPR lanes; 0.171 -> 0.168 ms at 65,536 worlds); in the crowded
 // build the same copy costs 4.69 -> 5.19 ms, so it reads the kernel argument.
 template <int RM>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_step(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_step(
     uint8_t *state, int n, int max_m, size_t row_bytes, D1Config cfg, D1Tables tab, const int64_t *actions,
     uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
     __shared__ Smem sm;
