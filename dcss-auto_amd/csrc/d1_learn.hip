@@ -610,6 +610,14 @@ __device__ __forceinline__ void primitive_learn(LCtx &c, int d, int limit, POut 
         uint64_t movers = ballot(alive && x.mawake && x.menergy >= 80 && cheb(x.mpos, x.player) > 1);
         if (movers) bfs(x, movers, imax(2, (maxspeed + 9) / 10));
         while (x.hp > 0 && ballot(x.lane < REQ && x.menergy >= 80)) {   // no reduction once nobody can act
+            // the lane id opaque per act, so that the monster rules' lane-derived masks and
+            // addresses are recomputed in each act instead of held through the loop: 168 -> 121
+            // VGPRs, 3 -> 4 waves per SIMD, k_learn_step 0.903 -> 0.796 ms
+            {
+                int l = lane_id();
+                asm volatile("" : "+v"(l));
+                x.lane = l;
+            }
             const int key = wave_max(x.lane < REQ && x.menergy >= 80 ? x.menergy * 128 + 127 - x.lane : -1);
             int id = 127 - (key & 127);
             act(x, id);
@@ -991,7 +999,7 @@ __global__ __launch_bounds__(64) void k_learn_init(uint8_t *state, int n, D1Conf
     observe_learn(c, obs ? obs + (size_t)env * D1L_OBS : nullptr, mask ? mask + (size_t)env * D1L_ACTIONS : nullptr);
 }
 template <int CLUMP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_learn_step(uint8_t *state, int n, D1Config cfg, D1LTables t,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_learn_step(uint8_t *state, int n, D1Config cfg, D1LTables t,
                                                    const int64_t *actions, int limit, float *obs, float *mask,
                                                    float *out, const bool *active) {
     __shared__ LSmem L;
