@@ -3,7 +3,8 @@ requires of its kernels: "Custom kernels must honor the stream that produces act
 consumes observations" (gpu-d1/scripts/test_learning.py:62-69). Each call is made once under
 the default stream and once inside `with torch.cuda.stream(side)` on tensors created there,
 and the results must be identical bit for bit: Env.step (with a reset), LearnEnv.step and
-its controller, the fused policy forward + sample, and the PPO minibatch step."""
+its controller, the fused policy forward + sample (plain and autoregressive head), and the
+PPO minibatch step."""
 import importlib
 
 import numpy as np
@@ -89,6 +90,30 @@ def test_policy_forward_sample_on_a_side_stream():
         logits = torch.empty((n, P.N_ACTIONS), device='cuda')
         P.policy_fwd_sample(x, wpk, b1, b2, b3, 42, 9, actions, logp, value, logits=logits)
         return actions, logp, value, logits
+
+    want = run()
+    torch.cuda.synchronize()
+    got = on_side_stream(run)
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+
+
+def test_ar_policy_forward_sample_on_a_side_stream():
+    print('[streams] ar policy', flush=True)
+    P = importlib.import_module('dcss-auto_amd.policy')
+    model = P.ARPolicy(seed=6).cuda().to(torch.bfloat16)
+    model.packed()
+    g = torch.Generator(device='cuda').manual_seed(2)
+    obs = torch.randint(0, 30, (3001, 1800), dtype=torch.uint8, device='cuda', generator=g)
+
+    def run():
+        n = obs.shape[0]
+        x = obs.clone()
+        action = torch.empty(n, dtype=torch.int64, device='cuda')
+        logp, value = torch.empty(n, device='cuda'), torch.empty(n, device='cuda')
+        verb_logits = torch.empty((n, P.N_VERBS), device='cuda')
+        P.policy_fwd_sample_ar(x, model.packed(), 17, 5, action, logp, value, verb_logits=verb_logits)
+        return action, logp, value, verb_logits
 
     want = run()
     torch.cuda.synchronize()
