@@ -38,6 +38,7 @@ struct Smem {
             uint32_t lay1[ROWS_WORDS];
         };
         float stage[D1_STAGE_FLOATS];
+        uint32_t orow[30];   // the observation's 15 window rows, two words each (write_obs)
     };
     uint32_t rq[24];   // the repair search's queue (packed entries)
     // the player view when a kernel keeps it in LDS (Ctx::view_lds), quadrant q in words 2q

@@ -242,7 +242,9 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
         }
     }
     x.ticks++;
-    if (x.first_stair_tick < 0 && known_stairs(x) > 0) x.first_stair_tick = x.ticks;
+    // A stair becomes known only through a reveal: this turn's (a move) or the reset's, which
+    // runs after the previous turn's check (the first turn of an episode, ticks == 1).
+    if (x.first_stair_tick < 0 && (moved || x.ticks == 1) && known_stairs(x) > 0) x.first_stair_tick = x.ticks;
     bool death = x.hp <= 0, timeout = !clear && !death && x.ticks >= c->limit;
     if (clear) milli += c->clear_milli;
     if (death) milli -= c->death_milli;
@@ -291,15 +293,20 @@ __device__ __forceinline__ void transition(Ctx &x, int action, float *out, const
 // gpu-d1/branches/d1-stairs-v2/src/learn.cu:269-280).
 //
 // Lanes 0..14 build their window row (dy = lane - 7) as 15-bit strips (bit k = column
-// px - 7 + k): wall | viewed-floor << 16 in w0, visible | frontier << 16 in w1. A cell lane
-// then fetches its row's two words with one shuffle each and assembles its 8 bytes from
-// single bits; monsters and stairs in the window are applied by uniform loops. No LDS
-// writes and no barriers.
-__device__ __forceinline__ uint32_t row_strip15(Row r, int px) {   // bits px-7 .. px+7, zero outside 0..95
-    const int s = px - 7, k = s >> 5;                               // s >= -7, so k in -1..2
-    const uint32_t w0 = k == 0 ? r.a : k == 1 ? r.b : k == 2 ? r.c : 0u;
-    const uint32_t w1 = k == -1 ? r.a : k == 0 ? r.b : k == 1 ? r.c : 0u;
-    return __builtin_amdgcn_alignbit(w1, w0, (uint32_t)s & 31u) & 0x7FFFu;
+// px - 7 + k): wall | viewed-floor << 16 in w0, visible | frontier << 16 in w1, staged in
+// LDS. Each row is worked on as one 32-column window of the bitmaps (not their three
+// 32-bit words). A cell lane reads its row's pair and assembles its 8 bytes from single
+// bits; the lanes of the living monsters and of the known stairs then write their bytes
+// over their cells (loops over the window's monsters and stairs, each testing the four
+// cells of every lane, cost more than the rest of the observation at 8 monsters).
+// 32 columns of bitmap row y from column s (bit j = column s + j), s = 32k + sh with k the
+// uniform word index (-1..2): two adjacent words and one funnel shift. Left of the map (k = -1)
+// the low word is zero; right of it the high word is the next row's first. Bits of columns
+// outside 0..W-1 are arbitrary: every use masks them.
+__device__ __forceinline__ uint32_t win32(const uint32_t *bm, int y, int k, uint32_t sh) {
+    const uint32_t *w = bm + y * RW + imax(k, 0);
+    const uint32_t a = w[0], b = w[1];
+    return __builtin_amdgcn_alignbit(k < 0 ? a : b, k < 0 ? 0u : a, sh);
 }
 __device__ __forceinline__ void write_obs(Ctx &x, uint8_t *o) {
     Smem *sm = x.sm;
@@ -308,67 +315,62 @@ __device__ __forceinline__ void write_obs(Ctx &x, uint8_t *o) {
     {
         const int dy = x.lane - 7, y = py + dy;
         if (x.lane < 15 && y >= 0 && y < H) {
-            const Row all = row_range(0, W - 1);
-            Row u{0, 0, 0};
-            for (int yy = y - 1; yy <= y + 1; yy++)
-                if (yy >= 0 && yy < H) u = row_or(u, row_andn(all, row_ld(sm->viewed, yy)));
-            u = row_and(row_or(u, row_or(row_shl1(u), row_shr1(u))), all);
-            const Row vw = row_ld(sm->viewed, y), fl = row_ld(sm->floor, y);
-            const int klo = imax(0, 7 - px), khi = imin(14, W + 6 - px);
-            const uint32_t ib = ((2u << khi) - 1u) & ~((1u << klo) - 1u);
-            const uint32_t v = row_strip15(vw, px), f = row_strip15(fl, px);
-            const uint32_t fr = row_strip15(row_and(row_and(fl, vw), u), px) & ib;
+            // one 32-column window per row, s = px - 8: the window's columns px-7 .. px+7 are
+            // its bits 1..15, and bits 0 and 16 the columns the frontier's dilation reads
+            const int s = px - 8, k = s >> 5;
+            const uint32_t sh = (uint32_t)s & 31u;
+            const uint32_t ibx = ((2u << imin(31, W - 1 - s)) - 1u) & ~((1u << imax(0, -s)) - 1u);   // map columns
+            const uint32_t v0 = win32(sm->viewed, y, k, sh), f0 = win32(sm->floor, y, k, sh);
+            const uint32_t vm = y > 0 ? win32(sm->viewed, y - 1, k, sh) : ~0u;
+            const uint32_t vp = y < H - 1 ? win32(sm->viewed, y + 1, k, sh) : ~0u;
+            const uint32_t u = ~(vm & v0 & vp) & ibx;   // unviewed map cells in rows y-1 .. y+1
+            const uint32_t ud = u | (u << 1) | (u >> 1);
+            const uint32_t ib = (ibx >> 1) & 0x7FFFu;
             const int ay = iabs(dy);
             uint32_t R = 0, L = 0;
             if (dy >= 0) { R |= (uint32_t)(view_q(x, 0) >> (8 * ay)) & 0xFFu; L |= (uint32_t)(view_q(x, 1) >> (8 * ay)) & 0xFFu; }
             if (dy <= 0) { R |= (uint32_t)(view_q(x, 3) >> (8 * ay)) & 0xFFu; L |= (uint32_t)(view_q(x, 2) >> (8 * ay)) & 0xFFu; }
             const uint32_t vis = ((__builtin_bitreverse32(L) >> 24) | (R << 7)) & ib;
-            w0 = ((~ib | (v & ~f)) & 0x7FFFu) | ((v & f & ib) << 16);
-            w1 = vis | (fr << 16);
+            w0 = (((~ibx | (v0 & ~f0)) >> 1) & 0x7FFFu) | (((v0 & f0 & ibx) >> 1) & 0x7FFFu) << 16;
+            w1 = vis | (((v0 & f0 & ud & ibx) >> 1) & 0x7FFFu) << 16;
         }
     }
-    // the four cell chunks of this lane (cell c0 + lane, c0 = 0, 64, 128, 192)
-    const uint32_t php = (uint32_t)imin(imax(x.hp, 0), 255);
-    uint32_t lo[4], hi[4], vis[4], vf[4];
-    int cell[4];
+    // The row pairs go to LDS; a cell lane reads its row's pair (one LDS read a cell where two
+    // cross-lane shuffles were) and assembles its 8 bytes with two byte permutes.
+    if (x.lane < 15) { sm->orow[2 * x.lane] = w0; sm->orow[2 * x.lane + 1] = w1; }
+    __syncthreads();
+    const uint32_t php8 = (uint32_t)imin(imax(x.hp, 0), 255) << 8;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const int cidx = 64 * c + x.lane, r = cidx / 15, k = cidx - 15 * r;
-        const uint32_t a = (uint32_t)__shfl((int)w0, imin(r, 14)) >> k, b = (uint32_t)__shfl((int)w1, imin(r, 14)) >> k;
-        cell[c] = cidx;
-        vis[c] = b & 1u;
-        vf[c] = (a >> 16) & 1u;
-        lo[c] = (a & 1u) | vf[c] << 8 | vis[c] << 16;
-        hi[c] = php << 8 | ((b >> 16) & 1u) << 24;
+        const uint32_t cidx = 64u * c + (uint32_t)x.lane;
+        if (cidx >= 225u) continue;
+        const uint32_t r = (cidx * 4370u) >> 16, k = cidx - 15u * r;   // cidx / 15, exact below 256
+        const uint32_t a = (sm->orow[2 * r] >> k) & 0x10001u, b = (sm->orow[2 * r + 1] >> k) & 0x10001u;
+        // bytes 0-3 wall, viewed floor, visible, 0 (a's bytes 0 and 2, b's byte 0);
+        // bytes 4-7 0, player HP, 0, frontier (b's byte 2)
+        const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0c040200u), hi = __builtin_amdgcn_perm(b, php8, 0x060c010cu);
+        *(uint2 *)(o + cidx * 8) = make_uint2(lo, hi);
     }
-    // living monsters inside the window: each monster lane computes its cell and bytes once,
-    // then the owner lane of that cell takes them when the cell is visible
-    int mc = -1;
+    // The cells' few other bytes are written over them by the lanes that own the facts. One
+    // wave's memory operations take effect in program order, so a wavefront-scope fence (a
+    // compiler barrier) is all the ordering these second stores need.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // a living monster on a visible window cell: kind + 1 and HP (living monsters hold
+    // distinct cells)
     if (x.lane < x.c->count && x.mhp > 0) {
         const int dx = x.mpos % W - px, dy = x.mpos / W - py;
-        if (iabs(dx) <= 7 && iabs(dy) <= 7) mc = (dy + 7) * 15 + dx + 7;
+        if (iabs(dx) <= 7 && iabs(dy) <= 7 && ((sm->orow[2 * (dy + 7) + 1] >> (dx + 7)) & 1u)) {
+            uint8_t *q = o + ((dy + 7) * 15 + dx + 7) * 8;
+            q[3] = (uint8_t)(x.mkind + 1);
+            q[4] = (uint8_t)imin(x.mhp, 255);
+        }
     }
-    const uint32_t mlo = (uint32_t)(x.mkind + 1) << 24, mhi = (uint32_t)imin(x.mhp, 255);
-    for (uint64_t m = ballot(mc >= 0); m; m &= m - 1) {
-        const int i = __ffsll((unsigned long long)m) - 1;
-        const int ci = lane_val(mc, i), c = ci >> 6;
-        const uint32_t ol = (uint32_t)lane_val((int)mlo, i), oh = (uint32_t)lane_val((int)mhi, i);
-#pragma unroll
-        for (int cc = 0; cc < 4; cc++)
-            if (cc == c && cell[cc] == ci && vis[cc]) { lo[cc] |= ol; hi[cc] |= oh; }
+    // a known stair on a viewed floor window cell (lane k: stair k)
+    if (x.lane < 3) {
+        const int sp = (int16_t)(uint16_t)(x.stairs >> (16 * x.lane)), dx = sp % W - px, dy = sp / W - py;
+        if (sp >= 0 && iabs(dx) <= 7 && iabs(dy) <= 7 && ((sm->orow[2 * (dy + 7)] >> (dx + 23)) & 1u))
+            o[((dy + 7) * 15 + dx + 7) * 8 + 6] = 1;
     }
-    // known stairs inside the window mark a viewed floor cell
-    for (int k = 0; k < 3; k++) {
-        const int sp = stair_at(x, k), dx = sp % W - px, dy = sp / W - py;
-        if (sp < 0 || iabs(dx) > 7 || iabs(dy) > 7) continue;
-        const int ci = (dy + 7) * 15 + dx + 7, c = ci >> 6;
-#pragma unroll
-        for (int cc = 0; cc < 4; cc++)
-            if (cc == c && cell[cc] == ci && vf[cc]) hi[cc] |= 1u << 16;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-        if (cell[c] < 225) *(uint2 *)(o + cell[c] * 8) = make_uint2(lo[c], hi[c]);
 }
 // Sum over canonical words of fmix32(word ^ index*0x9E3779B9) (index map in
 // include/d1hip.h's companion spec: scalars 0-14, monsters 100+2i, viewed 1000+3y+j).
