@@ -217,16 +217,17 @@ __device__ __noinline__ uint32_t philox_lane(uint32_t key0, uint32_t key1, uint3
     return j == 0 ? c0 : j == 1 ? c1 : j == 2 ? c2 : c3;
 }
 
-constexpr uint32_t RNG_EMPTY = 0x80000000u;   // a buffer base no draw index reaches
-
 struct Rng {
     uint64_t st, inc;                   // PCG32: the state before draw `sb`
     uint32_t key0, key1, t, env, dom;   // counter stream
-    uint32_t k;                         // index of the next draw
-    uint32_t sb, base;                  // PCG state index; draw index held by lane 0
-    uint32_t buf;                       // lane l: draw base + l
+    uint32_t base, o;                   // lane l of buf holds draw base + l; the next draw is base + o
+    uint32_t sb;                        // PCG state index
+    uint32_t buf;
     int mode;
 
+    __device__ __forceinline__ uint32_t k() const { return base + o; }   // index of the next draw
+    // Draw values are a function of their index alone, so the buffer may be refilled at any
+    // index: a fill that comes early changes no value.
     __device__ __forceinline__ void fill(uint32_t at) {
         int lane = (int)threadIdx.x;
         if (mode == 0) {
@@ -238,21 +239,39 @@ struct Rng {
             buf = philox_lane(key0, key1, t, env, dom, at + (uint32_t)lane);
         }
         base = at;
+        o = 0;
     }
     __device__ __forceinline__ uint32_t next() {
-        if (k - base >= 64u) fill(k);
-        uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)buf, (int)(k - base));
-        k++;
+        if (o >= 64u) fill(base + o);
+        uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)buf, (int)o);
+        o++;
         return v;
+    }
+    // A rule that makes at most n draws reserves them: the buffer is refilled now if fewer
+    // than n remain, and its draws (RES) skip the per-draw buffer check.
+    __device__ __forceinline__ void reserve(uint32_t n) {
+        if (o > 64u - n) fill(base + o);
+    }
+    template <bool RES>
+    __device__ __forceinline__ uint32_t take() {
+        if (RES) {
+            uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)buf, (int)o);
+            o++;
+            return v;
+        }
+        return next();
     }
     // PCG32 state before draw k (what the sequential generator would hold now)
     __device__ __forceinline__ uint64_t pcg_state() const {
-        uint32_t j = k - sb;
+        uint32_t j = base + o - sb;
         return kJump.a[j] * st + kJump.c[j] * inc;
     }
-    __device__ __forceinline__ int r(int bound) {   // gpu-d1/src/sim.h:36-51
+    // gpu-d1/src/sim.h:36-51. Inside a reservation of n (RES), a rejected draw's redraws are
+    // checked draws and the reservation is renewed after them.
+    template <bool RES = false, uint32_t NRES = 0>
+    __device__ __forceinline__ int r(int bound) {
         if (bound <= 1) return 0;
-        uint32_t x = next();
+        uint32_t x = take<RES>();
         uint64_t m = (uint64_t)x * (uint32_t)bound;
         uint32_t low = (uint32_t)m;
         if (low < (uint32_t)bound) {
@@ -262,13 +281,16 @@ struct Rng {
                 m = (uint64_t)x * (uint32_t)bound;
                 low = (uint32_t)m;
             }
+            if (RES) reserve(NRES);
         }
         return (int)(m >> 32);
     }
-    __device__ __forceinline__ int avg(int n) { int a = r(n); return (a + r(n + 1)) / 2; }             // sim.h:52-55
-    __device__ __forceinline__ int round(int n, int d) { int rem = n % d; return n / d + (rem && r(d) < rem); }  // sim.h:56-59
+    template <bool RES = false, uint32_t NRES = 0>
+    __device__ __forceinline__ int avg(int n) { int a = r<RES, NRES>(n); return (a + r<RES, NRES>(n + 1)) / 2; }   // sim.h:52-55
+    template <bool RES = false, uint32_t NRES = 0>
+    __device__ __forceinline__ int round(int n, int d) { int rem = n % d; return n / d + (rem && r<RES, NRES>(d) < rem); }  // sim.h:56-59
     __device__ __forceinline__ void pcg_load(uint64_t state, uint64_t increment) {
-        mode = 0; st = state; inc = increment; k = 0; sb = 0; base = RNG_EMPTY;
+        mode = 0; st = state; inc = increment; sb = 0; base = 0u - 64u; o = 64;   // next draw 0, buffer empty
     }
     __device__ __forceinline__ void pcg_seed(uint64_t s, uint64_t seq) {   // sim.h:29-35: two steps around +s
         uint64_t i = (seq << 1) | 1;
@@ -279,7 +301,7 @@ struct Rng {
     }
     __device__ __forceinline__ void counter(uint64_t key, uint32_t e, uint32_t tt, uint32_t d) {
         mode = 1; key0 = (uint32_t)key; key1 = (uint32_t)(key >> 32); env = e; t = tt; dom = d;
-        k = 0; sb = 0; base = RNG_EMPTY; st = 0; inc = 0;
+        sb = 0; base = 0u - 64u; o = 64; st = 0; inc = 0;
     }
 };
 
@@ -295,7 +317,7 @@ __device__ __forceinline__ int reservoir(Rng &s, int total, int lane) {
     while (c0 <= total) {
         int cnt = imin(64, total - c0 + 1);
         int c = c0 + lane;
-        if (s.base != s.k) s.fill(s.k);
+        if (s.o != 0) s.fill(s.k());
         uint64_t m = (uint64_t)s.buf * (uint32_t)c;
         bool act = lane < cnt;
         bool risky = act && (uint32_t)m < (uint32_t)c;
@@ -304,7 +326,7 @@ __device__ __forceinline__ int reservoir(Rng &s, int total, int lane) {
         } else {
             uint64_t keep = ballot(act && (m >> 32) == 0);
             if (keep) chosen = c0 + 63 - __clzll((long long)keep) - 1;
-            s.k += (uint32_t)cnt;
+            s.o += (uint32_t)cnt;
         }
         c0 += cnt;
     }
@@ -343,6 +365,7 @@ struct Ctx {
     // stored field belongs to (-1: none), and the player cell whose field LDS holds (-1: none)
     uint32_t *fcache = nullptr;
     int ftag = -1, fld = -1;
+    bool rfloor = false;   // the memo's reach bitmap is the floor bitmap (not stored)
     // rows of the viewed bitmap changed since the world was loaded (vlo > vhi: none); the
     // default, every row, is what a world that was not loaded from a state row writes back
     int vlo = 0, vhi = H - 1;
@@ -540,24 +563,29 @@ __device__ __forceinline__ int kind_speed(const D1Config *c, int k) {
 // gpu-d1/src/sim.h:130-163 (kind = the acting monster's kind)
 __device__ __forceinline__ void attack(Ctx &x, int kind) {
     const D1Config *c = x.c;
-    const D1Kind &k = c->kinds[kind];
+    // every configuration value the attack may need, read before its first branch
+    const D1Kind k = c->kinds[kind];
+    const int ac100 = c->ac100, ev100 = c->ev100, sh100 = c->sh100, shield_limit = c->shield_limit;
+    const int gdr0 = c->gdr[0], gdr1 = c->gdr[1];
     Rng &r = x.g;
-    int hit = r.r(k.tohit + 1);
-    int ev = r.round(c->ev100, 100);
-    ev = r.avg(2 * ev);
+    constexpr uint32_t ND = 15;   // the most draws an attack makes without a rejection
+    r.reserve(ND);
+    int hit = r.r<true, ND>(k.tohit + 1);
+    int ev = r.round<true, ND>(ev100, 100);
+    ev = r.avg<true, ND>(2 * ev);
     int margin = hit - ev;
-    if (r.r(100) < 5) margin = (r.r(2) ? 1 : -1) * 1000;
-    int bypass = r.r(k.bypass);
-    int sh = r.round(c->sh100, 100);
-    int block = r.avg(sh * 2) / 3 - 1;
-    if (block >= bypass && x.blocks < c->shield_limit) { x.blocks++; return; }
+    if (r.r<true, ND>(100) < 5) margin = (r.r<true, ND>(2) ? 1 : -1) * 1000;
+    int bypass = r.r<true, ND>(k.bypass);
+    int sh = r.round<true, ND>(sh100, 100);
+    int block = r.avg<true, ND>(sh * 2) / 3 - 1;
+    if (block >= bypass && x.blocks < shield_limit) { x.blocks++; return; }
     if (margin < 0) return;
-    int damage = 1 + r.r(k.damage);
-    int ac = r.round(c->ac100, 100);
-    int gac = r.round(c->ac100, 100);
-    int gdr = c->gdr[imin(imax(gac - c->ac100 / 100, 0), 1)];
-    int saved = r.r(ac + 1);
-    int half = r.round(ac, 2);
+    int damage = 1 + r.r<true, ND>(k.damage);
+    int ac = r.round<true, ND>(ac100, 100);
+    int gac = r.round<true, ND>(ac100, 100);
+    int gdr = imin(imax(gac - ac100 / 100, 0), 1) ? gdr1 : gdr0;
+    int saved = r.r<true, ND>(ac + 1);
+    int half = r.round<true, ND>(ac, 2);
     saved = imax(saved, imin(gdr * k.damage / 100, half));
     damage = imax(0, damage - saved);
     x.hp -= damage;

@@ -52,9 +52,10 @@ __host__ __device__ constexpr int off_viewed(int m) { return OFF_MON + 8 * m; }
 __host__ __device__ constexpr int off_floor(int m) { return off_viewed(m) + ROWS_WORDS * 4; }
 __host__ __device__ constexpr int off_cells(int m) { return off_floor(m) + ROWS_WORDS * 4; }
 // Layouts with more than 8 monsters also keep the distance-field memo: dword 0 the player
-// cell it was computed for (-1: none), dword 1 its last layer, dwords 2-33 the monsters'
-// absolute layers (int16 each, 32767 = unknown), dwords 34-49 the monsters' stuck-cache
-// radii (uint8 each, 0 = none; Ctx::mrad), then the reach, lay0 and lay1 bitmaps.
+// cell it was computed for (-1: none), dword 1 its last layer (bit 31: the reach bitmap
+// equals the floor bitmap and is not stored), dwords 2-33 the monsters' absolute layers
+// (int16 each, 32767 = unknown), dwords 34-49 the monsters' stuck-cache radii (uint8 each,
+// 0 = none; Ctx::mrad), then the reach, lay0 and lay1 bitmaps.
 constexpr int FC_RAD = 34, FC_HEAD = 50, FC_DWORDS = FC_HEAD + 3 * ROWS_WORDS;
 __host__ __device__ constexpr bool has_fcache(int m) { return m > 8; }
 __host__ __device__ constexpr int off_fcache(int m) { return off_cells(m) + ROWS_WORDS * 4; }
@@ -134,14 +135,19 @@ __device__ __forceinline__ void reset(Ctx &x, const uint32_t *cells_g) {
 // layouts keep a complete field (BFS to exhaustion, every living monster's layer recorded)
 // in the state row and reuse it while the player stays on that cell; monster moves keep
 // their layers exact (a move is to a reached neighbour, one of -1/0/+1 away). A step whose
-// player stands still then reads 2,520 bytes instead of running the whole BFS.
+// player stands still then reads 1,680 bytes (2,520 where the level is not connected)
+// instead of running the whole BFS.
 __device__ __forceinline__ void field_memo(Ctx &x) {
     if (x.fld == x.player) return;   // LDS holds it already (a REST repeat)
     Smem *sm = x.sm;
     uint32_t *fc = x.fcache;
     if (x.ftag == x.player) {
+        if (x.rfloor) {
+            for (int w = x.lane; w < ROWS_WORDS; w += 64) sm->reach[w] = sm->floor[w];
+        } else {
+            for (int w = x.lane; w < ROWS_WORDS; w += 64) sm->reach[w] = fc[FC_HEAD + w];
+        }
         for (int w = x.lane; w < ROWS_WORDS; w += 64) {
-            sm->reach[w] = fc[FC_HEAD + w];
             sm->lay0[w] = fc[FC_HEAD + ROWS_WORDS + w];
             sm->lay1[w] = fc[FC_HEAD + 2 * ROWS_WORDS + w];
             sm->front[w] = 0;   // the repair search's queued marks start clear, as after bfs()
@@ -150,8 +156,14 @@ __device__ __forceinline__ void field_memo(Ctx &x) {
     } else {
         const uint64_t living = ballot(x.lane < x.c->count && x.mhp > 0);
         bfs(x, living, BIG);
+        // On a connected level the complete field reaches every floor cell: the reach plane
+        // is then not stored, and a reload takes the floor bitmap for it (840 bytes less each
+        // way).
+        bool same = true;
+        for (int w = x.lane; w < ROWS_WORDS; w += 64) same = same && sm->reach[w] == sm->floor[w];
+        x.rfloor = !ballot(!same);
         for (int w = x.lane; w < ROWS_WORDS; w += 64) {
-            fc[FC_HEAD + w] = sm->reach[w];
+            if (!x.rfloor) fc[FC_HEAD + w] = sm->reach[w];
             fc[FC_HEAD + ROWS_WORDS + w] = sm->lay0[w];
             fc[FC_HEAD + 2 * ROWS_WORDS + w] = sm->lay1[w];
         }
@@ -421,7 +433,7 @@ __device__ __forceinline__ void store_world(Ctx &x, uint8_t *row, int max_m) {
     for (int w = RW * x.vlo + x.lane; w < RW * (x.vhi + 1); w += 64) vg[w] = x.sm->viewed[w];
     if (has_fcache(max_m)) {   // memo head: its player cell, last layer, the monsters' layers
         uint32_t *fc = (uint32_t *)(row + off_fcache(max_m));
-        if (x.lane == 0) { fc[0] = (uint32_t)x.ftag; fc[1] = (uint32_t)x.lastl; }
+        if (x.lane == 0) { fc[0] = (uint32_t)x.ftag; fc[1] = (uint32_t)x.lastl | (uint32_t)x.rfloor << 31; }
         if (x.lane < max_m) {
             ((int16_t *)(fc + 2))[x.lane] = (int16_t)imin(x.mlay, 32767);
             ((uint8_t *)(fc + FC_RAD))[x.lane] = (uint8_t)imin(x.mrad, 255);
@@ -530,7 +542,9 @@ __device__ __forceinline__ void unpack_world(Ctx &x, const Pre &pf, int max_m) {
     x.vlo = H, x.vhi = -1;   // no viewed row changed yet
     if (has_fcache(max_m)) {
         x.ftag = (int)__builtin_amdgcn_readlane((int)pf.fh, 0);
-        x.lastl = (int)__builtin_amdgcn_readlane((int)pf.fh, 1);
+        const uint32_t h1 = (uint32_t)__builtin_amdgcn_readlane((int)pf.fh, 1);
+        x.lastl = (int)(h1 & 0x7FFFFFFFu);
+        x.rfloor = h1 >> 31;
         const uint32_t pair = (uint32_t)__shfl((int)pf.fh, 2 + (x.lane >> 1));
         const int ml = (int16_t)(x.lane & 1 ? pair >> 16 : pair & 0xFFFFu);
         x.mlay = ml >= 32767 ? FAR : ml;
