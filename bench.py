@@ -5,7 +5,9 @@ training loop, C5 and the CPU baseline beside it.
 One step = one pass over 65,536 worlds: the HIP env step (transition + auto-reset +
 15x15x8 uint8 observation) and the fused HIP policy kernel (bf16 MLP 1800->256->256 with a
 16-logit head and a value head on MFMA, then the counter-RNG categorical sample of the next
-actions). Inputs stay resident in HBM; the timed region is bracketed by synchronisations.
+actions). The worlds run as two row ranges of 32,768, each a step -> policy pipeline on its
+own stream (`--streams 1`: one range, one stream). Inputs stay resident in HBM; the timed
+region is bracketed by synchronisations.
 Prints one JSON line: C3 decisions/s as `value`, then `ppo` (C4 samples/s, median of three
 updates after a warm one), `train` (rollout + update iterations), `stress` (C5 at 262,144
 worlds with 40 monsters) and `cpu_baseline` (C1 on the CPU restatement at 1 thread and at
@@ -232,6 +234,11 @@ def wait_bench(args, worlds=8192, count=8, chunk=64, waits=4096):
                        'waits_per_kernel': chunk, 'waits_per_world': waits}, 'seconds': dt}
 
 
+def row_ranges(n, k):
+    """k contiguous row ranges covering 0..n-1."""
+    return [(n * j // k, n * (j + 1) // k) for j in range(k)]
+
+
 def event_stride(steps):
     """Timed steps per sampled set of per-kernel HIP events: every 8th step of a long run
     (three event records per step cost the measured loop ~4%), every 2nd of a short one so
@@ -416,6 +423,9 @@ def main():
     ap.add_argument('--no-ppo', action='store_true', help='rollout mode: skip the C4 PPO and training measurements that follow')
     ap.add_argument('--no-stress', action='store_true', help='rollout mode: skip the C5 stress measurement that follows')
     ap.add_argument('--ppo-updates', type=int, default=3, help='timed C4 updates (after one warm update); median reported')
+    ap.add_argument('--streams', type=int, default=2, choices=(1, 2),
+                    help='rollout and counters modes: the worlds as this many row ranges, each stepped and sampled '
+                         'on its own stream (default 2)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)', file=sys.stderr)
@@ -455,11 +465,14 @@ def main():
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
+        parts = row_ranges(n, args.streams)   # the rollout's launches: one per row range
         for t in range(args.steps):
             actions.random_(0, 16)
-            env.step(actions)
+            for lo, hi in parts:
+                env.step_rows(lo, hi, actions)
         torch.cuda.synchronize()
-        print(json.dumps({'mode': 'counters', 'copy_bytes': src.numel() * 4, 'env_steps': args.steps, 'envs': n}))
+        print(json.dumps({'mode': 'counters', 'copy_bytes': src.numel() * 4, 'env_steps': args.steps, 'envs': n,
+                          'worlds_per_launch': n // args.streams}))
         return
 
     if args.mode == 'ppo':
@@ -469,35 +482,63 @@ def main():
     wpk, b1, b2, b3 = model.packed()
     value = torch.empty(n, dtype=torch.float32, device=dev)
 
-    def one_step(t, ev=None):   # env step, then forward + counter-RNG sample in one kernel
-        if ev is not None:
-            ev[0].record()
-        env.step(actions)
-        if ev is not None:
-            ev[1].record()
-        policy_mod.policy_fwd_sample(env.obs.view(n, -1), wpk, b1, b2, b3, seed, t, actions, logp, value)
-        if ev is not None:
-            ev[2].record()
+    # The worlds as `streams` row ranges, each a pipeline of its own on its own stream (every
+    # stream at the default priority): env step, then forward + counter-RNG sample in one
+    # kernel. A range's next step depends only on its own actions, so the ranges' kernels
+    # overlap and fill one another's launch tails. Each range samples with its own key.
+    parts = row_ranges(n, args.streams)
+    streams = [torch.cuda.current_stream()] if len(parts) == 1 else [torch.cuda.Stream() for _ in parts]
+    obs = env.obs.view(n, -1)
 
+    def one_step(t, ev=None):
+        for j, ((lo, hi), st) in enumerate(zip(parts, streams)):
+            with torch.cuda.stream(st):
+                if ev is not None:
+                    ev[j][0].record()
+                env.step_rows(lo, hi, actions)
+                if ev is not None:
+                    ev[j][1].record()
+                policy_mod.policy_fwd_sample(obs[lo:hi], wpk, b1, b2, b3, seed + 7919 * j, t, actions[lo:hi],
+                                             logp[lo:hi], value[lo:hi])
+                if ev is not None:
+                    ev[j][2].record()
+
+    torch.cuda.synchronize()   # the new streams start after the set-up on the default one
     for t in range(args.warmup):
         one_step(t)
     torch.cuda.synchronize()
-    # per-kernel HIP events on every EVERY-th step of the timed region: an event record costs
-    # the stream a few microseconds, so events around every launch would slow the
-    # throughput being measured (three per step: ~4%)
+    # per-kernel HIP events (on each range's own stream) on every EVERY-th step of the timed
+    # region: an event record costs the stream a few microseconds, so events around every
+    # launch would slow the throughput being measured (three per step: ~4%). With two
+    # ranges the launches share the GPU with the other range's, and their durations say so.
     every = event_stride(args.steps)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, every)]
+    events = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in parts]
+              for _ in range(0, args.steps, every)]
     t0 = time.perf_counter()
     for k in range(args.steps):
         one_step(args.warmup + k, events[k // every] if k % every == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    step_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
-    trunk_ms = sum(e[1].elapsed_time(e[2]) for e in events) / len(events)
+    flat = [e for per_step in events for e in per_step]
+    step_ms = sum(e[0].elapsed_time(e[1]) for e in flat) / len(flat)
+    trunk_ms = sum(e[1].elapsed_time(e[2]) for e in flat) / len(flat)
     decisions = n * args.steps / wall
+    # The kernels alone (outside the timed region): whole-batch launches on one stream, with
+    # nothing else on the GPU, for the per-kernel rooflines beside the pipeline's
+    iso = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(8)]
+    for k, e in enumerate(iso):
+        e[0].record()
+        env.step(actions)
+        e[1].record()
+        policy_mod.policy_fwd_sample(obs, wpk, b1, b2, b3, seed, args.warmup + args.steps + k, actions, logp, value)
+        e[2].record()
+    torch.cuda.synchronize()
+    iso_step_ms = sum(e[0].elapsed_time(e[1]) for e in iso) / len(iso)
+    iso_trunk_ms = sum(e[1].elapsed_time(e[2]) for e in iso) / len(iso)
     step_bytes = STEP_BYTES.get(args.monsters, 3270)
-    achieved = step_bytes * n / (step_ms * 1e-3) / 1e9
-    trunk_tflops = TRUNK_FLOPS * n / (trunk_ms * 1e-3) / 1e12
+    per_launch = n // len(parts)
+    achieved = step_bytes * per_launch / (step_ms * 1e-3) / 1e9
+    trunk_tflops = TRUNK_FLOPS * per_launch / (trunk_ms * 1e-3) / 1e12
     result = {
         'metric': 'env decisions/sec at 65,536 envs (1 GPU): step+obs+policy+sample',
         'value': decisions,
@@ -513,10 +554,19 @@ def main():
         'data': 'synthetic: generated 80x70 levels, random-init N(0,0.02) bf16 policy',
         'config': {'workload': 'C3', 'envs': n, 'monsters': args.monsters, 'obs': '15x15x8 uint8',
                    'policy': '1800-256-256 ReLU, 16 logits + value, bf16', 'sampler': 'Philox counter RNG',
-                   'rollout_steps': args.steps},
-        'roofline': roofline('d1::k_step', achieved, step_ms, step_bytes, measured_traffic(), len(events)),
+                   'rollout_steps': args.steps,
+                   'pipeline': f'{len(parts)} row ranges of {per_launch} worlds, one stream each'},
+        'roofline': dict(roofline('d1::k_step', achieved, step_ms, step_bytes, measured_traffic(), len(flat)),
+                         worlds_per_launch=per_launch,
+                         isolated={'worlds_per_launch': n, 'avg_launch_ms': iso_step_ms,
+                                   'achieved': step_bytes * n / (iso_step_ms * 1e-3) / 1e9,
+                                   'frac': step_bytes * n / (iso_step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                   'launches': len(iso), 'note': 'one stream, after the timed region'}),
         'trunk': {'bound': 'mfma', 'achieved': trunk_tflops, 'peak': BF16_PEAK_TFLOPS, 'unit': 'TFLOP/s',
-                  'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms},
+                  'frac': trunk_tflops / BF16_PEAK_TFLOPS, 'avg_ms': trunk_ms, 'rows_per_launch': per_launch,
+                  'isolated': {'rows_per_launch': n, 'avg_ms': iso_trunk_ms,
+                               'achieved': TRUNK_FLOPS * n / (iso_trunk_ms * 1e-3) / 1e12,
+                               'frac': TRUNK_FLOPS * n / (iso_trunk_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}},
     }
     if not args.no_ppo:   # the metric's second number: C4 PPO samples/s, measured after the rollout
         ppo = ppo_bench(args, env, model, policy_mod, dev)

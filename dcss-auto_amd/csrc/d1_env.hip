@@ -616,15 +616,23 @@ __global__ __launch_bounds__(64) void k_init(uint8_t *state, int n, int max_m, s
 // world, which shortens the tail in which a few slow worlds (resets, long monster turns)
 // run on an otherwise idle chip (k_step 193 -> 187 us at 65,536 worlds). WPB is 4 for the
 // <= 8 monster build (0.176 -> 0.171 ms at 65,536 worlds) and 3 for the crowded build
-// (C5 k_step: 2 worlds 3.38 ms, 3 worlds 3.35, 4 worlds 3.37).
-constexpr int STEP_TAIL = 8192, STEP_WPB = 4, CROWD_WPB = 3;
-__host__ __device__ inline int step_groups(int n, int wpb) { return (n - (n < STEP_TAIL ? n : STEP_TAIL)) / wpb; }
-__host__ __device__ inline int step_blocks(int n, int wpb) { const int g = step_groups(n, wpb); return g + (n - wpb * g); }
+// (C5 k_step: 2 worlds 3.38 ms, 3 worlds 3.35, 4 worlds 3.37). The <= 8 monster build's tail
+// is 4,096 worlds: the C3 rollout steps its 65,536 worlds as two ranges of 32,768 on two
+// streams, where the other range's kernels fill the idle CUs (rollout 364.7 -> 375.7 M
+// decisions/s against a tail of 8,192; 0: 368.2, 2,048: 374.3); the crowded build keeps 8,192
+// (C5 k_step 2.063 ms against 2.090 with 4,096).
+constexpr int STEP_TAIL = 4096, CROWD_TAIL = 8192, STEP_WPB = 4, CROWD_WPB = 3;
+__host__ __device__ inline int step_groups(int n, int wpb, int tail) { return (n - (n < tail ? n : tail)) / wpb; }
+__host__ __device__ inline int step_blocks(int n, int wpb, int tail) {
+    const int g = step_groups(n, wpb, tail);
+    return g + (n - wpb * g);
+}
 template <int RM, int WPB, bool CROWD>
 __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int max_m, size_t row_bytes,
                                             const D1Config *cfgp, const D1Tables &tab, const int64_t *actions,
                                             uint8_t *obs, float *out, uint32_t *hash, const uint8_t *active) {
-    const int g = step_groups(n, WPB), blk = (int)blockIdx.x;   // first < n for every block of step_blocks(n, WPB)
+    constexpr int TAIL = CROWD ? CROWD_TAIL : STEP_TAIL;
+    const int g = step_groups(n, WPB, TAIL), blk = (int)blockIdx.x;   // first < n for every block of step_blocks
     const int first = blk < g ? WPB * blk : WPB * g + (blk - g), last = imin(n, blk < g ? first + WPB : first + 1);
     Ctx x;
     x.sm = &sm; x.c = cfgp; x.rays = tab.ray_slots; x.nslots = tab.nslots; x.lane = lane_id();
@@ -963,7 +971,8 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
     auto kern = max_monsters > 8 ? (cfg->rng_mode == 0 ? d1::k_step_crowd<0> : d1::k_step_crowd<1>)
                                  : (cfg->rng_mode == 0 ? d1::k_step<0> : d1::k_step<1>);
     const int wpb = max_monsters > 8 ? d1::CROWD_WPB : d1::STEP_WPB;
-    hipLaunchKernelGGL(kern, dim3(d1::step_blocks(n, wpb)), dim3(64), 0, (hipStream_t)stream,
+    const int tail = max_monsters > 8 ? d1::CROWD_TAIL : d1::STEP_TAIL;
+    hipLaunchKernelGGL(kern, dim3(d1::step_blocks(n, wpb, tail)), dim3(64), 0, (hipStream_t)stream,
                        (uint8_t *)state, n, max_monsters,
                        (size_t)d1::state_bytes(max_monsters), *cfg, *tab, actions, obs, out, hash, active);
     return (int)hipGetLastError();

@@ -116,6 +116,22 @@ class Env:
                                     self.stream), 'd1_init')
         return self.obs
 
+    def step_rows(self, lo, hi, actions):
+        """Steps worlds lo..hi-1 only, with actions[lo:hi], writing their observation and
+        out rows (the hash is not computed), on the current stream. Disjoint row ranges are
+        independent, so they may be stepped on different streams."""
+        if not (actions.device == self.device and actions.dtype == torch.int64 and actions.is_contiguous()
+                and actions.shape == (self.batch,)):
+            raise ValueError('actions must be a contiguous int64 tensor of shape [batch] on the env device')
+        if not (0 <= lo < hi <= self.batch):
+            raise ValueError(f'row range [{lo}, {hi}) outside [0, {self.batch})')
+        rb = self.state.shape[1]
+        _lib.check(self.lib.d1_step(self.state.data_ptr() + lo * rb, hi - lo, self.max_monsters, C.byref(self.cfg),
+                                    C.byref(self.tables), actions.data_ptr() + lo * 8,
+                                    self.obs.data_ptr() + lo * 1800, self.out.data_ptr() + lo * 4 * self.out.shape[1],
+                                    None, None, self.stream), 'd1_step')
+        return self.obs[lo:hi], self.out[lo:hi]
+
     def step(self, actions, active=None, obs=None):
         """`obs` optionally redirects this step's observation into another uint8
         [batch, 15, 15, 8]-shaped buffer (e.g. a rollout-buffer slice); self.obs then

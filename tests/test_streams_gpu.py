@@ -51,6 +51,36 @@ def test_env_step_on_a_side_stream(pkg):
             assert torch.equal(a, b), f'step {k}'
 
 
+def test_env_row_ranges_on_two_streams(pkg):
+    """Env.step_rows: two disjoint row ranges stepped on two concurrent streams (the C3
+    bench's pipeline) give exactly the rows of whole-batch steps: each world's step reads
+    only its own row and action."""
+    print('[streams] row ranges', flush=True)
+    n, h = 3000, 1234   # uneven ranges, several workgroups each
+    cfg = pkg.baseline_config(8)
+    whole = pkg.Env(n, cfg, seed=17, hash=False)
+    split = pkg.Env(n, cfg, seed=17, hash=False)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    g = torch.Generator(device='cuda').manual_seed(9)
+    torch.cuda.synchronize()
+    for k in range(60):
+        a = torch.randint(0, 19, (n,), device='cuda', generator=g)
+        whole.step(a)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(sa):
+            split.step_rows(0, h, a)
+        with torch.cuda.stream(sb):
+            split.step_rows(h, n, a)
+        torch.cuda.synchronize()
+        assert torch.equal(whole.state, split.state), f'step {k}: state rows'
+        assert torch.equal(whole.obs, split.obs), f'step {k}: observations'
+        assert torch.equal(whole.out, split.out), f'step {k}: out rows'
+    with pytest.raises(ValueError):
+        split.step_rows(5, 5, a)
+    with pytest.raises(ValueError):
+        split.step_rows(0, n + 1, a)
+
+
 def test_learn_step_on_a_side_stream():
     print('[streams] learn', flush=True)
     L = importlib.import_module('dcss-auto_amd.learn')
