@@ -92,6 +92,11 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
 }
 // gpu-d1/src/sim.h:14
 __device__ __forceinline__ int cheb(int a, int b) { return imax(iabs(a % W - b % W), iabs(a / W - b / W)); }
+// the same for two cells of the map (0 <= a, b < N): unsigned division by the width is shorter
+__device__ __forceinline__ int cheb_u(int a, int b) {
+    const uint32_t ua = (uint32_t)a, ub = (uint32_t)b;
+    return imax(iabs((int)(ua % W) - (int)(ub % W)), iabs((int)(ua / W) - (int)(ub / W)));
+}
 // gpu-d1/src/sim.h:201-206: N, E, S, W, NE, SE, SW, NW
 __device__ __forceinline__ int nbr(int p, int d) {
     int ddx = d == 1 || d == 4 || d == 5 ? 1 : d == 3 || d == 6 || d == 7 ? -1 : 0;
@@ -800,7 +805,8 @@ __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, i
 __device__ __forceinline__ int choose_move(Ctx &x, int id, int p, int plag, int &qlag) {
     int rotation = x.g.r(4);
     const Smem *sm = x.sm;
-    const int px = p % W, py = p / W, plx = x.player % W, ply = x.player / W;
+    const int px = (int)((uint32_t)p % W), py = (int)((uint32_t)p / W);
+    const int plx = (int)((uint32_t)x.player % W), ply = (int)((uint32_t)x.player / W);
     const int mp = plag < FAR ? plag % 3 : 0;   // p's layer mod 3, as its bit planes hold it
     const int z = x.lane & 7;
     const int d = z < 4 ? (z + rotation) & 3 : 4 + ((z + rotation) & 3);
@@ -921,21 +927,21 @@ __device__ __forceinline__ void bfs(Ctx &x, uint64_t movers, int margin) {
 }
 // Cells a and b changed occupancy: stuck answers whose search read either are dropped.
 __device__ __forceinline__ void stuck_touch(Ctx &x, int a, int b) {
-    if (x.mrad > 0 && (cheb(x.mpos, a) <= x.mrad || cheb(x.mpos, b) <= x.mrad)) x.mrad = 0;
+    if (x.mrad > 0 && (cheb_u(x.mpos, a) <= x.mrad || cheb_u(x.mpos, b) <= x.mrad)) x.mrad = 0;
 }
 // gpu-d1/src/sim.h:254-269
 // The mover's absolute layer follows it (the cell it steps to is a reached neighbour).
 __device__ __forceinline__ void act(Ctx &x, int id) {
     if (x.lane == id) x.menergy -= 10;
     int p = lane_val(x.mpos, id);
-    if (cheb(p, x.player) == 1) { attack(x, lane_val(x.mkind, id)); return; }
+    if (cheb_u(p, x.player) == 1) { attack(x, lane_val(x.mkind, id)); return; }
     int qlag = FAR;
     int q = choose_move(x, id, p, lane_val(x.mlay, id), qlag);
     if (q >= 0) {
         if (x.lane == 0) {   // occupancy follows the monster (one lane, then a wave-wide wait)
-            uint32_t *occ = x.sm->occ;
-            occ[(p / W) * RW + ((p % W) >> 5)] &= ~(1u << ((p % W) & 31));
-            occ[(q / W) * RW + ((q % W) >> 5)] |= 1u << ((q % W) & 31);
+            const uint32_t up = (uint32_t)p, uq = (uint32_t)q;
+            atomicAnd(&x.sm->occ[(up / W) * RW + ((up % W) >> 5)], ~(1u << ((up % W) & 31)));
+            atomicOr(&x.sm->occ[(uq / W) * RW + ((uq % W) >> 5)], 1u << ((uq % W) & 31));
         }
         if (x.stuck_cache) stuck_touch(x, p, q);   // the mover's own entry too (p is its cell)
         __syncthreads();

@@ -215,7 +215,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
     bool clear = (d == 18 && stair_index(x) > 0 && x.hp > 0) || (c->clear_on_kill_all && x.killed == c->count);
     if (!clear) {
         bool mine = x.lane < c->count;
-        uint64_t cand = ballot(mine && x.mhp > 0 && !x.mawake && cheb(x.mpos, x.player) <= 6);
+        uint64_t cand = ballot(mine && x.mhp > 0 && !x.mawake && cheb_u(x.mpos, x.player) <= 6);
         while (cand) {
             int i = __ffsll((unsigned long long)cand) - 1;
             cand &= cand - 1;
@@ -225,7 +225,7 @@ __device__ __forceinline__ bool primitive(Ctx &x, int d, float *out8, bool &saw,
         if (mine && x.mhp > 0 && !x.mawake) x.menergy = -30000;
         if (mine && x.mhp > 0) x.menergy += kind_speed(c, x.mkind);
         x.menergy = (int16_t)x.menergy;
-        uint64_t movers = ballot(mine && x.mhp > 0 && x.mawake && x.menergy >= 80 && cheb(x.mpos, x.player) > 1);
+        uint64_t movers = ballot(mine && x.mhp > 0 && x.mawake && x.menergy >= 80 && cheb_u(x.mpos, x.player) > 1);
         if (movers) {
             if (x.fcache) field_memo(x);
             else {
