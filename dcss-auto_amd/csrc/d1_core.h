@@ -804,6 +804,10 @@ __device__ __forceinline__ bool detour_ruled_out(const Ctx &x, int px, int py, i
 // cell's layer goes to qlag.
 __device__ __forceinline__ int choose_move(Ctx &x, int id, int p, int plag, int &qlag) {
     int rotation = x.g.r(4);
+    // A cached stuck answer stands for the whole choice: the player has not moved and no cell
+    // within its radius (1 or more, so the eight neighbours too) changed occupancy, so no
+    // neighbour is lower and the detour finds nothing, as when the answer was recorded.
+    if (x.stuck_cache && lane_val(x.mrad, id) > 0) return -1;
     const Smem *sm = x.sm;
     const int px = (int)((uint32_t)p % W), py = (int)((uint32_t)p / W);
     const int plx = (int)((uint32_t)x.player % W), ply = (int)((uint32_t)x.player / W);
@@ -828,7 +832,6 @@ __device__ __forceinline__ int choose_move(Ctx &x, int id, int p, int plag, int 
     }
     // With no walkable neighbour the search would queue nothing after p and find nothing.
     if (!x.c->repair || !ballot(c.walk)) return -1;
-    if (x.stuck_cache && lane_val(x.mrad, id) > 0) return -1;   // still stuck
     int rad = 0;
     if (detour_ruled_out(x, px, py, plx, ply, mp, rad)) {
         if (x.stuck_cache && x.lane == id) x.mrad = rad;
