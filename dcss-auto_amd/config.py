@@ -155,3 +155,18 @@ def shared_map_arrays():
     floor = m['floor'].astype(np.uint8)
     cells = ((floor != 0) & (m['dist'] < 65535)).astype(np.uint8)
     return floor, cells
+
+
+def check_level(floor, cells):
+    """A shared level given as (floor, cells) masks -> two contiguous uint8 [5600] arrays
+    of 0/1; raises ValueError on a wrong size, or on a spawnable cell that is not floor."""
+    floor = np.ascontiguousarray(floor, np.uint8).reshape(-1)
+    cells = np.ascontiguousarray(cells, np.uint8).reshape(-1)
+    if floor.size != 5600 or cells.size != 5600:
+        raise ValueError('a level is 80 x 70 = 5600 cells')
+    floor, cells = (floor != 0).astype(np.uint8), (cells != 0).astype(np.uint8)
+    if np.any(cells > floor):
+        raise ValueError('spawnable cells must be floor cells')
+    if not cells.any():
+        raise ValueError('a level needs at least one spawnable cell')
+    return floor, cells

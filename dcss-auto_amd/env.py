@@ -67,7 +67,11 @@ def decode_rows(raw, max_monsters):
 
 
 class Env:
-    def __init__(self, batch=512, cfg=None, seed=0, device='cuda', max_monsters=None, hash=True):
+    def __init__(self, batch=512, cfg=None, seed=0, device='cuda', max_monsters=None, hash=True, level=None):
+        """`level` optionally replaces map 1057 as the shared level (level_mode shared): a
+        (floor, cells) pair of 5600-byte 0/1 masks, row-major 80 x 70, where cells (the
+        spawnable cells, a subset of the floor) is what player, monsters and stairs are
+        placed on."""
         self.with_hash = hash
         self.device = torch.device('cuda:0' if device == 'cuda' else device)
         if self.device.type != 'cuda':
@@ -80,7 +84,7 @@ class Env:
             raise RuntimeError('D1Config layout differs from the library')
         r = data.rays()
         self.ray_slots = torch.from_numpy(r['slots'].view(np.int64).copy()).to(self.device)
-        floor, cells = cfgmod.shared_map_arrays()
+        floor, cells = cfgmod.shared_map_arrays() if level is None else cfgmod.check_level(*level)
         self.floor = torch.from_numpy(floor).to(self.device)
         self.cells = torch.from_numpy(cells).to(self.device)
         self.tables = cfgmod.D1Tables(self.floor.data_ptr(), self.cells.data_ptr(), self.ray_slots.data_ptr(),

@@ -51,13 +51,13 @@ def ptr(a):
 class OracleEnv:
     """Batch of worlds stepped by the CPU restatement; numpy buffers mirror the GPU Env."""
 
-    def __init__(self, batch, cfg, seed=0, threads=1):
+    def __init__(self, batch, cfg, seed=0, threads=1, level=None):
         self.L, self.batch, self.cfg, self.threads = lib(), batch, cfg, threads
         self.state = np.zeros((batch, self.L.o_state_bytes()), np.uint8)
         self.obs = np.zeros((batch, 15, 15, 8), np.uint8)
         self.out = np.zeros((batch, 8), np.float32)
         self.hash = np.zeros(batch, np.uint32)
-        self.floor, self.cells = pkg.shared_map_arrays()
+        self.floor, self.cells = pkg.shared_map_arrays() if level is None else pkg.config.check_level(*level)
         self.reset(seed)
 
     def reset(self, seed):

@@ -111,3 +111,60 @@ def test_crowded_field_memo_standing_player(pkg):
         cpu.step(a)
         gpu.step(torch.from_numpy(a).to(gpu.device))
         compare(gpu, cpu, k, 'crowded memo')
+    tag, whole = memo_heads(gpu)
+    assert (tag >= 0).any() and (whole[tag >= 0] == 1).all()    # generated levels are connected
+
+
+def memo_heads(env):
+    """The crowded rows' distance-field memo head (after the header, view, monsters and the
+    viewed, floor and cells bitmaps): the player cell the stored field is for (-1: none)
+    and bit 31 of its second dword, set when the stored field reaches the whole floor and
+    its reach plane is not stored."""
+    off = 96 + 8 * env.max_monsters + 3 * 840
+    head = env.state[:, off:off + 8].cpu().numpy().copy().view('<u4')
+    return head[:, 0].view('<i4'), head[:, 1] >> 31
+
+
+def pocket_level(pkg):
+    """Map 1057 plus a 3 x 3 floor pocket walled off from the rest (rows 7-9, columns
+    38-40, two wall cells from the nearest floor): floor that no search from the player
+    reaches and that is not spawnable."""
+    floor, cells = pkg.shared_map_arrays()
+    f = floor.reshape(70, 80).copy()
+    assert not f[5:12, 36:43].any()    # the pocket and a two-cell wall ring around it
+    f[7:10, 38:41] = 1
+    return f.reshape(-1), cells
+
+
+@pytest.mark.parametrize('count', [8, 24])
+def test_level_with_an_unreachable_floor_pocket(pkg, count):
+    """On a level whose floor is not one connected region, the distance field reaches less
+    than the whole floor, so the crowded layouts store the reach plane with the field
+    instead of taking the floor bitmap for it. Worlds driven mostly by WAIT and REST (most
+    steps reload the stored field), with moves now and then: state rows, hash, out[] and
+    the observation equal the oracle's every step, in the <= 8 monster and the crowded
+    builds."""
+    print(f'[parity] pocket level count={count}', flush=True)
+    cfg = pkg.reference_config(count)
+    level = pocket_level(pkg)
+    n = 64
+    gpu = pkg.Env(n, cfg, seed=21, level=level)
+    cpu = O.OracleEnv(n, cfg, seed=21, threads=8, level=level)
+    assert gpu.floors().sum(1).tolist() == [int(level[0].sum())] * n
+    compare(gpu, cpu, -1, 'pocket')
+    rng = np.random.default_rng(8)
+    dones = stored = 0
+    for k in range(240):
+        if k % 3 == 0:
+            a = cpu.heuristic()
+        else:
+            a = np.where(rng.random(n) < 0.7, rng.choice([16, 17], n), rng.integers(0, 19, n)).astype(np.int64)
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, f'pocket{count}')
+        dones += int(cpu.out[:, 1].sum())
+        if count > 8:
+            tag, whole = memo_heads(gpu)
+            assert not whole[tag >= 0].any(), f'step {k}: a stored field claims to reach the pocket'
+            stored += int((tag >= 0).sum())
+    assert dones > 0 and (count == 8 or stored > 0)

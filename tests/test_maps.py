@@ -93,3 +93,22 @@ def test_native_export_parses_to_the_package_map(maps):
     los = maps.native_los(REF / 'native-1057')
     fixture = maps.read_fixture(REF / 'fixture.bin')
     assert np.array_equal(los, fixture['los'])
+
+
+def test_shared_level_checks():
+    """The optional shared level of Env(level=...): 5600-cell masks, spawnable cells inside
+    the floor, at least one spawnable cell; map 1057 passes unchanged."""
+    config = importlib.import_module('dcss-auto_amd.config')
+    floor, cells = config.shared_map_arrays()
+    f, c = config.check_level(floor, cells)
+    assert np.array_equal(f, floor) and np.array_equal(c, cells)
+    f2, c2 = config.check_level(floor.reshape(70, 80) * 3, cells.astype(bool))
+    assert np.array_equal(f2, floor) and np.array_equal(c2, cells)
+    with pytest.raises(ValueError, match='5600'):
+        config.check_level(floor[:5599], cells[:5599])
+    bad = cells.copy()
+    bad[np.flatnonzero(floor == 0)[0]] = 1
+    with pytest.raises(ValueError, match='floor'):
+        config.check_level(floor, bad)
+    with pytest.raises(ValueError, match='spawnable'):
+        config.check_level(floor, np.zeros(5600, np.uint8))
