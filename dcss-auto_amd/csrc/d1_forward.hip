@@ -236,11 +236,14 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
     __shared__ __align__(16) uint8_t lds[AR ? LDS_BYTES_AR : LDS_BYTES];
     const int t = threadIdx.x, lane = t & 63, lr = lane & 31, lh = lane >> 5;
     u32x4 *stage = (u32x4 *)lds;                           // W1 double buffer, later W2 + head
-    uint16_t *bl = (uint16_t *)(lds + LDS_W);              // [0,256) b1, [256,512) b2, [512,544) head bias
+    uint16_t *bl = (uint16_t *)(lds + LDS_W);              // [0,256) b1, [256,512) b2 (both permuted, below), [512,544) head bias
     const int m0 = blockIdx.x * BM + 64 * (t >> 6);
 
-    bl[t] = b1[t];
-    bl[256 + t] = b2[t];
+    {   // b1 and b2 in conversion order: unit 32b + 8g + 4h + i at 32b + 16h + 4g + i
+        const int u = t, pu = (u & ~31) + 16 * ((u >> 2) & 1) + 4 * ((u >> 3) & 3) + (u & 3);
+        bl[pu] = b1[u];
+        bl[256 + pu] = b2[u];
+    }
     if (t < 32) bl[512 + t] = t < NZ ? b3[t] : 0;
     if (AR && t < TH + 32) bl[544 + t] = t < TH + NT ? ar.bt[t] : 0;
 
@@ -392,13 +395,17 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
     // bias + ReLU + bf16 rounding (hardware pack) of acc into B fragments: fragment s of sample block a takes
     // registers 8(s%2)..+7 of tile (a, s/2); register 4g + i is hidden unit 32b + 8g + 4lh + i
     bf16x8 hf[2][16];
+    // (bias: this layer's 256 values in conversion order, the 16 of block b and lane half h
+    // contiguous at 32b + 16h)
     auto to_frags = [&](const uint16_t *bias) {
 #pragma unroll
-        for (int b = 0; b < 8; b++)
+        for (int b = 0; b < 8; b++) {
+            const u32x4 r0 = *(const u32x4 *)(bias + 32 * b + 16 * lh), r1 = *(const u32x4 *)(bias + 32 * b + 16 * lh + 8);
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const u32x2 bw = *(const u32x2 *)(bias + 32 * b + 8 * g + 4 * lh);
-                const float bb[4] = {bf(bw.x & 0xFFFFu), bf(bw.x >> 16), bf(bw.y & 0xFFFFu), bf(bw.y >> 16)};
+                const uint32_t bx = g == 0 ? r0.x : g == 1 ? r0.z : g == 2 ? r1.x : r1.z;
+                const uint32_t by = g == 0 ? r0.y : g == 1 ? r0.w : g == 2 ? r1.y : r1.w;
+                const float bb[4] = {bf(bx & 0xFFFFu), bf(bx >> 16), bf(by & 0xFFFFu), bf(by >> 16)};
 #pragma unroll
                 for (int a = 0; a < 2; a++) {
                     const int s = 2 * b + (g >> 1), j0 = 4 * (g & 1);
@@ -408,6 +415,7 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
                     hf[a][s] = as_bf(w);
                 }
             }
+        }
     };
     // stage W2 + head (contiguous in the packed buffer) into LDS in 3 rounds of 12 pieces;
     // the h1 conversion runs while the first two rounds are in flight
