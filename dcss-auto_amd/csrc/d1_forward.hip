@@ -238,6 +238,10 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
     u32x4 *stage = (u32x4 *)lds;                           // W1 double buffer, later W2 + head
     uint16_t *bl = (uint16_t *)(lds + LDS_W);              // [0,256) b1, [256,512) b2 (both permuted, below), [512,544) head bias
     const int m0 = blockIdx.x * BM + 64 * (t >> 6);
+    // the sampler's step, read now: loaded where it is used, at the end, its latency was
+    // the last thing every workgroup waited for (the AR build keeps the late load, which
+    // costs it no registers through the trunk)
+    const uint32_t tstep = SAMPLE ? (t_dev ? *t_dev : 0u) + t_add : 0u;
 
     {   // b1 and b2 in conversion order: unit 32b + 8g + 4h + i at 32b + 16h + 4g + i
         const int u = t, pu = (u & ~31) + 16 * ((u >> 2) & 1) + 4 * ((u >> 3) & 3) + (u & 3);
@@ -490,12 +494,13 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
     floatx16 z[2] = {};
     {
         const u32x4 *w3 = stage + 8 * 16 * 64 + lane;
+        bf16x8 fw[16];   // all 16 head fragments read first: one LDS wait instead of sixteen
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const bf16x8 fw = as_bf(w3[s * 64]);
+        for (int s = 0; s < 16; s++) fw[s] = as_bf(w3[s * 64]);
 #pragma unroll
-            for (int a = 0; a < 2; a++) z[a] = mfma(fw, hf[a][s], z[a]);
-        }
+        for (int s = 0; s < 16; s++)
+#pragma unroll
+            for (int a = 0; a < 2; a++) z[a] = mfma(fw[s], hf[a][s], z[a]);
     }
     const uint16_t *b3l = bl + 512;
     // the head output is bf16 (rounded once after the bias), widened to fp32; for sample block
@@ -519,7 +524,6 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
         // lane half h samples block a = h: it keeps its own half of that block's row and
         // receives the other half from its partner lane (l ^ 32), which sends the half of
         // the partner's own block that this lane lacks
-        const uint32_t tstep = (t_dev ? *t_dev : 0u) + t_add;
         // value blends by mask (a ternary between array elements is turned into a run-time
         // index into a stack copy of the array)
         const uint32_t hm = 0u - (uint32_t)lh;
