@@ -20,7 +20,9 @@
 //            of layer 2 takes registers 8(s%2)..8(s%2)+7 of tile (a, s/2) as its B operand
 //            slots j = 0..7. Slot j of half h in step s therefore stands for hidden unit
 //            k(s, h, j) = 32(s/2) + 16(s%2) + 8(j/4) + 4h + j%4, and W2 is packed in that
-//            order. W2 and the head weights (144 KB) are staged in LDS once per workgroup.
+//            order. W2 and the head weights (144 KB) are staged in LDS once per workgroup,
+//            in three rounds by K step, the last one in flight during layer 2's first 12
+//            steps.
 //   head     the same for h2 against a 32-row head (rows 17..31 zero).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -421,31 +423,30 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
             }
         }
     };
-    // stage W2 + head (contiguous in the packed buffer) into LDS in 3 rounds of 12 pieces;
-    // the h1 conversion runs while the first two rounds are in flight
-    {
-        constexpr int RND = NSTAGE / 256 / 3;
-        u32x4 v[RND];
-        auto sload = [&](int r) {
+    // stage W2 + head into LDS in 3 rounds of 12 pieces per lane, by K step: round 0 holds
+    // W2's steps 0..5, round 1 steps 6..11, round 2 steps 12..15 and the head. Rounds 0 and 1
+    // are in flight during the h1 conversion; round 2 is in flight during layer 2's first 12
+    // steps and is stored after them.
+    constexpr int RND = NSTAGE / 256 / 3;
+    static_assert(RND == 12 && NSTAGE == 8 * 16 * 64 + 16 * 64, "three rounds of 3,072 pieces");
+    auto spiece = [&](int r, int i) {   // piece of round r, item i (the same index in wpk and in LDS)
+        const int q = t + 256 * i;
+        if (r == 2 && q >= 2048) return 8 * 16 * 64 + (q - 2048);   // the head
+        return ((q >> 6 & 7) * 16 + 6 * r + (q >> 9)) * 64 + (q & 63);
+    };
+    u32x4 sv[RND], sv1[RND];
 #pragma unroll
-            for (int i = 0; i < RND; i++) v[i] = *(const u32x4 *)(wpk + PW2 + (size_t)(t + 256 * (RND * r + i)) * 8);
-        };
-        auto sstore = [&](int r) {
+    for (int i = 0; i < RND; i++) sv[i] = *(const u32x4 *)(wpk + PW2 + (size_t)spiece(0, i) * 8);
 #pragma unroll
-            for (int i = 0; i < RND; i++) stage[t + 256 * (RND * r + i)] = v[i];
-        };
-        u32x4 v1[RND];   // the second round is in flight with the first
-        sload(0);
+    for (int i = 0; i < RND; i++) sv1[i] = *(const u32x4 *)(wpk + PW2 + (size_t)spiece(1, i) * 8);
+    to_frags(bl);
 #pragma unroll
-        for (int i = 0; i < RND; i++) v1[i] = *(const u32x4 *)(wpk + PW2 + (size_t)(t + 256 * (RND + i)) * 8);
-        to_frags(bl);
-        sstore(0);
+    for (int i = 0; i < RND; i++) stage[spiece(0, i)] = sv[i];
 #pragma unroll
-        for (int i = 0; i < RND; i++) stage[t + 256 * (RND + i)] = v1[i];
-        sload(2);
-        sstore(2);
-    }
-    __syncthreads();   // staged weights visible
+    for (int i = 0; i < RND; i++) stage[spiece(1, i)] = sv1[i];
+#pragma unroll
+    for (int i = 0; i < RND; i++) sv[i] = *(const u32x4 *)(wpk + PW2 + (size_t)spiece(2, i) * 8);
+    __syncthreads();   // rounds 0 and 1 visible
 
     // ---- layer 2
 #pragma unroll
@@ -454,8 +455,7 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
         for (int b = 0; b < 8; b++) acc[a][b] = floatx16{};
     {
         const u32x4 *w2 = stage + lane;
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
+        auto l2step = [&](int s) {
             bf16x8 fw[8];
 #pragma unroll
             for (int b = 0; b < 8; b++) fw[b] = as_bf(w2[(b * 16 + s) * 64]);
@@ -463,7 +463,14 @@ __global__ __launch_bounds__(256) void k_policy(const uint8_t *__restrict__ obs,
             for (int b = 0; b < 8; b++)
 #pragma unroll
                 for (int a = 0; a < 2; a++) acc[a][b] = mfma(fw[b], hf[a][s], acc[a][b]);
-        }
+        };
+#pragma unroll
+        for (int s = 0; s < 12; s++) l2step(s);
+#pragma unroll
+        for (int i = 0; i < RND; i++) stage[spiece(2, i)] = sv[i];
+        __syncthreads();   // round 2 visible
+#pragma unroll
+        for (int s = 12; s < 16; s++) l2step(s);
     }
     if constexpr (AR) {
         // The AR pieces go where W2 was: their loads are in flight while h2 is converted,
