@@ -164,6 +164,12 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
     wload(wb[0], 0);
     wload(wb[1], 1);
     wload(wb[2], 2);
+    // the small operands of the later phases (biases, head weights), loaded now: the previous
+    // step's update wrote them from other XCDs, and loaded where they are used their latency
+    // was waited out in full at each phase
+    const uint16_t b1c = B1[c], b2c = B2[c], b3j = B3[t & 15], b3v = B3[NA];
+    const bf16x8 w3f0 = frag(wpk + P_W3, wave * 2, lane), w3f1 = frag(wpk + P_W3, wave * 2 + 1, lane);
+    const bf16x8 w3t0 = frag(wpk + P_W3T, wave * 2, lane), w3t1 = frag(wpk + P_W3T, wave * 2 + 1, lane);
     // the sample rows: their observation offsets go to LDS first, so that the row loads below
     // wait for one load level only; the per-sample scalars are loaded after the rows and
     // reach LDS at the barrier halfway through layer 1 (the loss reads them much later)
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
 #pragma unroll
         for (int q = 0; q < 16; q++) w2f[q] = frag(wpk + P_W2, wave * 16 + q, lane);   // layer 2's weights
         __syncthreads();   // every wave is done with the x rows before h1 overwrites them
-        const float bias = bf(B1[c]);
+        const float bias = bf(b1c);
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = fmaxf(e0[r] + e1[r] + bias, 0.f);
         rows_out(v, x1, w.h1f, nch, m0, c, lh, &mask1);
@@ -276,7 +282,7 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         }
 #pragma unroll
         for (int q = 0; q < 16; q++) w2f[q] = frag(wpk + P_W2T, wave * 16 + q, lane);   // dh1's weights
-        const float bias = bf(B2[c]);
+        const float bias = bf(b2c);
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = fmaxf(e0[r] + e1[r] + bias, 0.f);
         rows_out(v, x2, w.h2f, nch, m0, c, lh, &mask2);
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const uint4 av = *(const uint4 *)(x2 + lr * XS + 32 * wave + 16 * s + 8 * lh);
-            zacc = mfma(as_bf(av), frag(wpk + P_W3, wave * 2 + s, lane), zacc);
+            zacc = mfma(as_bf(av), s ? w3f1 : w3f0, zacc);
         }
         if (lr < NZ) {
 #pragma unroll
@@ -304,8 +310,8 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         float zj = zp[0][r][j], zv = zp[0][r][NA];
 #pragma unroll
         for (int q = 1; q < 8; q++) zj += zp[q][r][j], zv += zp[q][r][NA];
-        const float l = bf(rb(zj + bf(B3[j])));         // the head output is bf16
-        const float value = bf(rb(zv + bf(B3[NA])));
+        const float l = bf(rb(zj + bf(b3j)));         // the head output is bf16
+        const float value = bf(rb(zv + bf(b3v)));
         if (a.z_out) {
             a.z_out[(size_t)(m0 + r) * NZ + j] = l;
             if (j == 0) a.z_out[(size_t)(m0 + r) * NZ + NA] = value;
@@ -385,7 +391,7 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const uint4 av = *(const uint4 *)(dzs + lr * DS + 16 * s + 8 * lh);
-            acc = mfma(as_bf(av), frag(wpk + P_W3T, wave * 2 + s, lane), acc);
+            acc = mfma(as_bf(av), s ? w3t1 : w3t0, acc);
         }
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = (mask2 >> r) & 1u ? acc[r] : 0.f;
