@@ -76,9 +76,20 @@ struct Work {
 };
 
 __device__ __forceinline__ int64_t clamp_index(int64_t s, int64_t n) { return s < 0 ? 0 : (s >= n ? n - 1 : s); }
-__device__ __forceinline__ bool cursor_ok(const D1PPOStep &a) {
-    const int cur = a.cursor[0];
-    return cur >= 0 && (int64_t)(cur + 1) * a.mb <= a.n;
+// The cursor is read with a vector load (an agent-scope relaxed atomic load): a scalar load
+// is waited for together with the kernel-argument loads (scalar loads return out of order),
+// so every later instruction would wait for the cursor's round trip.
+__device__ __forceinline__ int load_cursor(const int32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool cursor_ok(const D1PPOStep &a, int cur) { return cur >= 0 && (int64_t)(cur + 1) * a.mb <= a.n; }
+__device__ __forceinline__ bool cursor_ok(const D1PPOStep &a) { return cursor_ok(a, load_cursor(a.cursor)); }
+// A cursor value `cur` (loaded early) made to depend on `after` (an empty asm): the check on
+// it, and the wait for its load, then come after the loads that produce `after`, which so
+// do not wait for the cursor's round trip.
+__device__ __forceinline__ int after(int cur, float after) {
+    asm volatile("" : "+v"(cur) : "v"(after));
+    return cur;
 }
 // fragment order for the uint8 x copy: 16-byte pieces, two per lane and chunk
 __device__ __forceinline__ size_t xidx(int row, int k, int nch) {
@@ -568,7 +579,9 @@ __device__ __forceinline__ void wgrad_tile2(const uint16_t *at, const void *bt, 
 // range of dh1 to every column tile.
 __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
     __shared__ uint4 bl[2 * 2 * 4 * 64];
-    if (!cursor_ok(a)) return;
+    // the cursor is checked before the stores only: the operand loads do not wait for it
+    // (past the end of the buffer the tiles multiply stale operands and store nothing)
+    const int cur = load_cursor(a.cursor);
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lr = lane & 31, lh = lane >> 5;
     const int mb = a.mb, nch = mb / 64, s1 = mb / KW;
     int b = blockIdx.x;
@@ -576,6 +589,7 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
         const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
         wgrad_tile2<true>(w.dh1f, w.xf, 2 * tile, XB, nch, split * (KW / 64), KW / 64, bl, acc);
+        if (!cursor_ok(a, after(cur, acc[0][0][0]))) return;
         float *out = w.part1 + (size_t)split * H * K1;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
@@ -592,6 +606,7 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
         const int tile = b / s1, split = b % s1;
         floatx16 acc[2][2] = {};
         wgrad_tile2<false>(w.dh2f, w.h1f, 2 * tile, 8, nch, split * (KW / 64), KW / 64, bl, acc);
+        if (!cursor_ok(a, after(cur, acc[0][0][0]))) return;
         float *out = w.part2 + (size_t)split * H * H;
 #pragma unroll
         for (int i = 0; i < 2; i++)
@@ -608,6 +623,7 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
     {
         floatx16 acc[1][2] = {};
         wgrad_tile<1, 2, false, 3>(w.dzf, 0, 1, w.h2f, 2 * wave, 8, nch, b * (KW3 / 64), KW3 / 64, acc);
+        if (!cursor_ok(a, after(cur, acc[0][0][0]))) return;
         float *out = w.part3 + (size_t)b * NZ * H;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++)
@@ -665,12 +681,16 @@ __device__ __forceinline__ float store_grad4(uint16_t *dst, float4 s) {
 
 __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
     __shared__ float red[256];
-    const bool ok = cursor_ok(a);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        a.cursor[1] = ok ? 1 : 0;   // k_adam reads this instead of the cursor it advances
-        if (ok) a.step[1] = a.step[0] + 1.f;
-    }
-    if (!ok) return;
+    // Past the end of the buffer nothing is stored (the partial loads do not wait for the
+    // cursor); workgroup 0 records the decision in cursor[1], which k_adam reads instead of the
+    // cursor it advances.
+    const int cur = load_cursor(a.cursor);
+    auto done = [&](bool ok) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            a.cursor[1] = ok ? 1 : 0;
+            if (ok) a.step[1] = a.step[0] + 1.f;
+        }
+    };
     const int t = threadIdx.x, mb = a.mb, s1 = mb / KW;
     uint16_t *g = (uint16_t *)a.g;
     float sq = 0.f;
@@ -687,6 +707,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
             src = w.part2 + 4 * e, stride = (size_t)H * H, dst = g + a.off_w2 + 4 * e;
         }
         const float4 s = sum_parts(src, stride, s1);
+        if (!cursor_ok(a, after(cur, s.x))) return done(false);
         sq = store_grad4(dst, s);
     } else if (blockIdx.x < NRED) {
         // s3 = 4 s1 partials per unit: lane q of a quad sums partials q s1 .. q s1 + s1 - 1 in
@@ -704,6 +725,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
             src = w.part3 + 4 * e, stride = (size_t)NZ * H, dst = g + a.off_w3 + 4 * e;
         }
         const float4 s = sum_parts(src + (size_t)q * s1 * stride, stride, s1);
+        if (!cursor_ok(a, after(cur, s.x))) return done(false);
         float4 o[3];
 #pragma unroll
         for (int k = 0; k < 3; k++)
@@ -726,6 +748,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
             }
 #pragma unroll
         for (int o = 16; o; o >>= 1) s += __shfl_xor(s, o, 32);   // the column's 32 lanes, fixed order
+        if (!cursor_ok(a, after(cur, s))) return done(false);
         if (part == 0 && col < 2 * H + NZ) {
             const uint16_t hb = rb(s);
             uint16_t *dst = col < H ? g + a.off_b1 + col : col < 2 * H ? g + a.off_b2 + (col - H) : g + a.off_b3 + (col - 2 * H);
@@ -740,6 +763,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
     }
     const float tot = block_sum(sq, red);
     if (t == 0) w.npart[blockIdx.x] = tot;
+    done(true);
 }
 
 // ---------------------------------------------------------------- k_adam
@@ -786,7 +810,7 @@ __device__ __forceinline__ void pack_param(const D1PPOStep &a, uint16_t *wpk, in
 // before the first non-finite loss.
 __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     __shared__ float red[4];
-    if (a.cursor[1] == 0) return;
+    const int flag = load_cursor(a.cursor + 1);
     const uint16_t *g = (const uint16_t *)a.g;
     uint16_t *pb = (uint16_t *)a.pb;
     // this lane's four parameters (launched with one group per lane), loaded before the
@@ -799,6 +823,7 @@ __global__ __launch_bounds__(256) void k_adam(D1PPOStep a, Work w) {
     static_assert(NRED + NBIASB > 512 && NRED + NBIASB <= 768, "three norm partials per lane");
     const int j = threadIdx.x;   // blockDim.x == 256; the three loads are in flight together
     const float n0 = w.npart[j], n1 = w.npart[j + 256], n2 = j + 512 < NRED + NBIASB ? w.npart[j + 512] : 0.f;
+    if (after(flag, n0) == 0) return;   // checked once the loads above are in flight
     const float acc = ((0.f + n0) + n1) + n2;
     const float norm = sqrtf(block_sum(acc, red));
     if (!(norm <= 3.4028235e38f) || a.step[2] != 0.f) {   // NaN fails the comparison

@@ -233,7 +233,8 @@ int d1_obs_to_bf16(const uint8_t *obs, void *out_bf16, int64_t count, void *stre
  * Minibatch i = cursor[0] covers samples perm[i*mb .. i*mb+mb) of the rollout buffer; each
  * call advances cursor[0] on the device, so a captured graph of several calls walks
  * consecutive minibatches. A call whose minibatch would end past n changes nothing.
- * Graph-safe: no memsets, no atomics; every reduction has a fixed order (bit-reproducible).
+ * Graph-safe: no memsets, no atomic read-modify-writes; every reduction has a fixed order
+ * (bit-reproducible).
  *
  * Parameters live in flat buffers (element offsets off_* into p / pb / g / m / v, each a
  * multiple of 8): l1.weight [256,1800], l1.bias [256], l2.weight [256,256], l2.bias [256],

@@ -326,10 +326,16 @@ def test_fast_ppo_graph_replays_match_eager():
             assert torch.equal(eager.step_t, graphed.step_t)
             assert torch.equal(eager.cursor[:1], graphed.cursor[:1])
     assert graphed.cursor[0].item() == n // mb
-    before = graphed.flat.p.clone()
+    # past the end: the kernels still load their operands (only their stores wait for the
+    # cursor check), and no output or state changes
+    F = graphed.flat
+    before = [x.clone() for x in (F.p, F.pb, F.g, F.m, F.v, graphed.step_t, graphed.loss_parts)]
     graphed._g.replay()
     torch.cuda.synchronize()
-    assert torch.equal(graphed.flat.p, before) and graphed.cursor[0].item() == n // mb
+    after = (F.p, F.pb, F.g, F.m, F.v, graphed.step_t, graphed.loss_parts)
+    for name, x, y in zip(('p', 'pb', 'g', 'm', 'v', 'step', 'loss_parts'), before, after):
+        assert torch.equal(x, y), name
+    assert graphed.cursor[0].item() == n // mb
 
 
 def test_fast_ppo_update_tracks_autograd_ppo():
