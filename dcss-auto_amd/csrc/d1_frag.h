@@ -25,6 +25,43 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Reductions over the 16 lanes of a DPP row (lane moves on the VALU instead of the LDS
+// crossbar __shfl_xor goes through), combining partners in the order of the __shfl_xor
+// butterfly with offsets 8, 4, 2, 1 and giving its results bit for bit: row_ror:8 is xor 8
+// within a row; after that step lanes l and l^8 hold equal values, so row_ror:4 reads one
+// holding lane l^4's value; quad_perm [2,3,0,1] and [1,0,3,2] are xor 2 and xor 1.
+constexpr int DPP_ROR8 = 0x128, DPP_ROR4 = 0x124, DPP_XOR2 = 0x4E, DPP_XOR1 = 0xB1;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f<DPP_ROR8>(x);
+    x += dpp_f<DPP_ROR4>(x);
+    x += dpp_f<DPP_XOR2>(x);
+    return x + dpp_f<DPP_XOR1>(x);
+}
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f<DPP_ROR8>(x));
+    x = fmaxf(x, dpp_f<DPP_ROR4>(x));
+    x = fmaxf(x, dpp_f<DPP_XOR2>(x));
+    return fmaxf(x, dpp_f<DPP_XOR1>(x));
+}
+
+// x + (x of lane l ^ 32) and x + (x of lane l ^ 16), bit for bit as with __shfl_xor (the
+// sum is commutative), through gfx950's lane-swap moves instead of the LDS crossbar:
+// v_permlane32_swap with x as both operands returns x's low half in every lane of its first
+// result and x's high half in every lane of its second (checked on the hardware);
+// v_permlane16_swap does the same for the even and odd 16-lane rows of each half.
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float bf(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 // float -> bf16, round to nearest even; NaNs stay NaN (quiet bit set when the dropped half
 // held the payload). Branch-free: in the epilogues this runs on hundreds of values per lane.

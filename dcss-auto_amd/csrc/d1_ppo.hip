@@ -139,7 +139,7 @@ __device__ __forceinline__ float rows_out(const float (&v)[16], uint16_t *tile, 
         *(uint2 *)(gf + fidx(c, m0 + 8 * g + 4 * lh, nch)) =
             make_uint2((uint32_t)hb[4 * g] | ((uint32_t)hb[4 * g + 1] << 16),
                        (uint32_t)hb[4 * g + 2] | ((uint32_t)hb[4 * g + 3] << 16));
-    return colsum + __shfl_xor(colsum, 32);
+    return xor32_sum(colsum);
 }
 
 __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
@@ -327,21 +327,12 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
             a.z_out[(size_t)(m0 + r) * NZ + j] = l;
             if (j == 0) a.z_out[(size_t)(m0 + r) * NZ + NA] = value;
         }
-        float mx = l;
-#pragma unroll
-        for (int o = 8; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-        float se = expf(l - mx);
-#pragma unroll
-        for (int o = 8; o; o >>= 1) se += __shfl_xor(se, o, 16);
+        const float mx = row16_max(l);   // reductions over the sample's 16 lanes
+        const float se = row16_sum(expf(l - mx));
         const float ls = logf(se);
         const float lp = l - mx - ls, p = expf(lp);
         const int act = sact[r];
-        float hh = -p * lp, la = j == act ? l : 0.f;
-#pragma unroll
-        for (int o = 8; o; o >>= 1) {
-            hh += __shfl_xor(hh, o, 16);
-            la += __shfl_xor(la, o, 16);
-        }
+        const float hh = row16_sum(-p * lp), la = row16_sum(j == act ? l : 0.f);
         const float lpa = la - mx - ls;
         const float ratio = expf(lpa - sold[r]);
         const float A = sadv[r];
@@ -360,21 +351,15 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         }
         // column sums of dz over this wave's 4 samples (lanes j, j+16, j+32, j+48)
         float cj = bf(dzj), cv = j == 0 ? bf(rb(a.vcoef * d * inv)) : 0.f;
-#pragma unroll
-        for (int o = 32; o >= 16; o >>= 1) {
-            cj += __shfl_xor(cj, o);
-            cv += __shfl_xor(cv, o);
-        }
+        cj = xor16_sum(xor32_sum(cj));
+        cv = xor16_sum(xor32_sum(cv));
         if (lane < 16) dzsum[wave][j] = cj;
         if (lane == 0) dzsum[wave][NA] = cv;
         // per-sample loss terms (every lane of a group holds them): lane j == 0 of each group
         float pg = j == 0 ? -fminf(un, cl) : 0.f, vl = j == 0 ? 0.5f * d * d : 0.f, ent = j == 0 ? hh : 0.f;
-#pragma unroll
-        for (int o = 32; o >= 16; o >>= 1) {
-            pg += __shfl_xor(pg, o);
-            vl += __shfl_xor(vl, o);
-            ent += __shfl_xor(ent, o);
-        }
+        pg = xor16_sum(xor32_sum(pg));
+        vl = xor16_sum(xor32_sum(vl));
+        ent = xor16_sum(xor32_sum(ent));
         if (lane == 0) lsum[wave][0] = pg, lsum[wave][1] = vl, lsum[wave][2] = ent;
     }
     __syncthreads();
@@ -386,8 +371,8 @@ __global__ __launch_bounds__(512) void k_rows(D1PPOStep a, Work w) {
         // the three loss sums also go to the bias-partial row's column 2H+NZ (k_reduce folds
         // their finiteness into the gradient norm)
         float z = s;
-        z += __shfl_xor(z, 1);
-        z += __shfl_xor(z, 2);
+        z += dpp_f<DPP_XOR1>(z);
+        z += dpp_f<DPP_XOR2>(z);
         if (t == 0) w.bpart[(size_t)blockIdx.x * BP + 2 * H + NZ] = z;
     } else if (t >= 64 && t < 64 + NZ) {   // head-bias partial: the 8 waves' sums
         float s = 0.f;
@@ -648,8 +633,7 @@ __global__ __launch_bounds__(256, 2) void k_wgrad(D1PPOStep a, Work w) {
 
 // ---------------------------------------------------------------- k_reduce
 __device__ __forceinline__ float block_sum(float x, float *red) {   // 256 lanes, red[4]
-#pragma unroll
-    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    x = row16_sum(xor16_sum(xor32_sum(x)));   // offsets 32, 16, then 8, 4, 2, 1
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
     __syncthreads();
     const float s = (red[0] + red[1]) + (red[2] + red[3]);
@@ -746,8 +730,7 @@ __global__ __launch_bounds__(256) void k_reduce(D1PPOStep a, Work w) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) s += x[j];
             }
-#pragma unroll
-        for (int o = 16; o; o >>= 1) s += __shfl_xor(s, o, 32);   // the column's 32 lanes, fixed order
+        s = row16_sum(xor16_sum(s));   // the column's 32 lanes, fixed order
         if (!cursor_ok(a, after(cur, s))) return done(false);
         if (part == 0 && col < 2 * H + NZ) {
             const uint16_t hb = rb(s);
