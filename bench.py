@@ -239,11 +239,12 @@ def row_ranges(n, k):
     return [(n * j // k, n * (j + 1) // k) for j in range(k)]
 
 
-def event_stride(steps):
+def event_stride(steps, launches_per_step=1):
     """Timed steps per sampled set of per-kernel HIP events: every 8th step of a long run
-    (three event records per step cost the measured loop ~4%), every 2nd of a short one so
-    that the kernel averages still rest on ten or more launches."""
-    return EVERY if steps >= 16 * EVERY else 2
+    (three event records per step cost the measured loop ~4%), and in a short one the widest
+    stride whose sampled steps still give each kernel ten or more timed launches
+    (`launches_per_step` launches of it per step)."""
+    return max(1, min(EVERY, steps * launches_per_step // 10))
 
 
 def roofline(kernel, achieved, launch_ms, step_bytes, traffic, launches):
@@ -511,7 +512,7 @@ def main():
     # region: an event record costs the stream a few microseconds, so events around every
     # launch would slow the throughput being measured (three per step: ~4%). With two
     # ranges the launches share the GPU with the other range's, and their durations say so.
-    every = event_stride(args.steps)
+    every = event_stride(args.steps, len(parts))
     events = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in parts]
               for _ in range(0, args.steps, every)]
     t0 = time.perf_counter()
