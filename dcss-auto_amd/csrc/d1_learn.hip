@@ -11,8 +11,8 @@
 //     are applied in the order the reference's refresh loop first touches them
 //     (key = position in the "each newly viewed cell, then its eight neighbours"
 //     sequence, taken by wave-min), appended or swap-removed through a per-window
-//     position table. Lists up to LCAP entries are staged in LDS, longer ones are
-//     worked on in place in the state row;
+//     position table. The list is worked on in place in the state row (through the
+//     caches: staging it in LDS and writing its changed part back cost more);
 //   * the known-floor BFS (viewed floor, from the player) is bit-parallel over LDS
 //     rows and stops once the nearest anchor layer and every remembered stair (or
 //     visible enemy, for the controller) is reached; route cues walk it backwards;
@@ -39,7 +39,6 @@ constexpr int O_ENEMY_HP = 225, O_RECORDS = 450, O_PLAYER = 650, O_RING = 654, O
               O_PROGRESS = 958, O_SLEEP = 959, O_STAIR = 999;
 constexpr int CLEAR_MILLI = 1000;
 constexpr float TURN_COST = 0.00001f;
-constexpr int LCAP = 1024;   // frontier entries staged in LDS
 constexpr int WIN = 17;      // 17x17 window in which a reveal can change anchors
 constexpr int INF = 0x7FFFFFFF;
 
@@ -64,7 +63,6 @@ constexpr int ROW_BYTES = (OFF_LIST + 2 * N + 63) / 64 * 64;
 struct LSmem {
     Smem s;                       // floor, viewed, occ (living enemies), reach, front, dist
     uint32_t anch[ROWS_WORDS];    // frontier anchors (then: anchors of the nearest BFS layer)
-    uint16_t list[LCAP];
     int16_t wslot[WIN * WIN];     // list position of anchors inside the window
     int32_t cbase[16];            // rank of the first newly viewed cell of each view row
 };
@@ -77,9 +75,7 @@ struct LCtx {
     int map_id, next_slot, nf;   // nf = frontier list length
     uint64_t enc;
     int mslot;             // this lane's enemy slot
-    uint16_t *glist, *lst; // the row's list; the list in use (LDS copy or the row)
-    bool lds;
-    int min_dirty;         // first list position changed since the load
+    uint16_t *lst;         // the row's frontier list
     int clumped, error;
 };
 
@@ -142,15 +138,6 @@ __device__ __forceinline__ int popc_below(Row r, int xx) {
     if (xx < 32) return __popc(r.a & ((1u << xx) - 1u));
     if (xx < 64) return __popc(r.a) + __popc(r.b & ((1u << (xx - 32)) - 1u));
     return __popc(r.a) + __popc(r.b) + __popc(r.c & ((1u << (xx - 64)) - 1u));
-}
-// Move the list from LDS to the state row (when it would outgrow LCAP).
-__device__ __forceinline__ void list_to_row(LCtx &c) {
-    for (int j = c.x.lane; j < c.nf; j += 64) c.glist[j] = c.L->list[j];
-    __threadfence_block();
-    __syncthreads();
-    c.lst = c.glist;
-    c.lds = false;
-    c.min_dirty = INF;   // the row is now current
 }
 
 // reveal (learn.cu:298-336): mark the view, count fresh floor, then replay the
@@ -225,9 +212,8 @@ __device__ __forceinline__ int reveal_learn(LCtx &c) {
         }
     }
     adds = (int)wave_sum((uint32_t)adds);
-    if (c.lds && c.nf + adds > LCAP) list_to_row(c);
     uint16_t *lst = c.lst;
-    int nf = c.nf, md = c.min_dirty;
+    int nf = c.nf;
     for (;;) {
         int lm = imin(imin(imin(key[0], key[1]), imin(key[2], key[3])), key[4]);
         int m = wave_min(lm);
@@ -243,10 +229,9 @@ __device__ __forceinline__ int reveal_learn(LCtx &c) {
         int q = (wy0 + wc / WIN) * W + wx0 + wc % WIN;
         // every lane performs the same uniform update, so each sees its own writes
         if (bit(L->anch, q)) {
-            if (nf >= (c.lds ? LCAP : N)) { c.error = 1; continue; }
+            if (nf >= N) { c.error = 1; continue; }
             lst[nf] = (uint16_t)q;
             L->wslot[wc] = (int16_t)nf;
-            md = imin(md, nf);
             nf++;
         } else {
             int s = L->wslot[wc];
@@ -256,12 +241,10 @@ __device__ __forceinline__ int reveal_learn(LCtx &c) {
             lst[s] = (uint16_t)r;
             int rx = r % W - wx0, ry = r / W - wy0;
             if (rx >= 0 && rx < WIN && ry >= 0 && ry < WIN) L->wslot[ry * WIN + rx] = (int16_t)s;
-            md = imin(md, s);
         }
     }
-    if (!c.lds) __threadfence_block();
+    __threadfence_block();
     c.nf = nf;
-    c.min_dirty = md;
     __syncthreads();
     int total = (int)wave_sum((uint32_t)fresh);
     x.floor_seen += total;
@@ -398,9 +381,6 @@ __device__ __forceinline__ void reset_learn(LCtx &c) {
         x.stairs = (x.stairs & ~(0xFFFFULL << (16 * k))) | (uint64_t)(uint16_t)sel << (16 * k);
     }
     c.nf = 0;
-    c.lst = c.L->list;
-    c.lds = true;
-    c.min_dirty = 0;
     reveal_learn(c);   // the initial view earns no reward
     update_knowledge(c);
 }
@@ -907,7 +887,7 @@ __device__ __forceinline__ int heuristic_learn(LCtx &c) {
 }
 
 // ---------------------------------------------------------------- load / store
-__device__ __forceinline__ void load_learn(LCtx &c, const uint8_t *row, bool list_too) {
+__device__ __forceinline__ void load_learn(LCtx &c, const uint8_t *row) {
     Ctx &x = c.x;
     const LHdr h = *(const LHdr *)row;
     x.g.pcg_load(h.rng_state, h.rng_inc);
@@ -930,13 +910,7 @@ __device__ __forceinline__ void load_learn(LCtx &c, const uint8_t *row, bool lis
     x.mpos = m.pos; x.mhp = m.hp; x.menergy = m.energy; x.mawake = m.awake; x.mkind = x.lane % 6; c.mslot = m.slot;
     const uint32_t *vg = (const uint32_t *)(row + OFF_VIEWED), *fg = (const uint32_t *)(row + OFF_FLOOR);
     for (int w = x.lane; w < ROWS_WORDS; w += 64) { x.sm->viewed[w] = vg[w]; x.sm->floor[w] = fg[w]; x.sm->occ[w] = 0; }
-    c.glist = (uint16_t *)(row + OFF_LIST);
-    c.min_dirty = INF;
-    c.lds = list_too && c.nf <= LCAP;
-    if (c.lds) {
-        for (int j = x.lane; j < c.nf; j += 64) c.L->list[j] = c.glist[j];
-        c.lst = c.L->list;
-    } else c.lst = c.glist;
+    c.lst = (uint16_t *)(row + OFF_LIST);
     __syncthreads();
     if (lane_alive(c)) occ_set_lane(x, x.mpos);
     __syncthreads();
@@ -962,8 +936,6 @@ __device__ __forceinline__ void store_learn(LCtx &c, uint8_t *row) {
     }
     uint32_t *vg = (uint32_t *)(row + OFF_VIEWED);
     for (int w = x.lane; w < ROWS_WORDS; w += 64) vg[w] = x.sm->viewed[w];
-    if (c.lds && c.min_dirty < c.nf)
-        for (int j = c.min_dirty + x.lane; j < c.nf; j += 64) c.glist[j] = c.L->list[j];
 }
 __device__ __forceinline__ void store_floor(LCtx &c, uint8_t *row) {
     uint32_t *fg = (uint32_t *)(row + OFF_FLOOR);
@@ -989,7 +961,7 @@ __global__ __launch_bounds__(64) void k_learn_init(uint8_t *state, int n, D1Conf
     D1LTables first = t;
     if (first.map_filter == -2) first.map_filter = env % first.n_maps;
     setup(c, &L, &cfg, &first);
-    c.glist = (uint16_t *)(row + OFF_LIST);
+    c.lst = (uint16_t *)(row + OFF_LIST);
     c.x.g.pcg_seed(mix64(seed + (uint64_t)env), (uint64_t)env + 1);
     c.x.episode = 0; c.x.decisions = 0;
     reset_learn<CLUMP>(c);
@@ -1009,7 +981,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     uint8_t *row = state + (size_t)env * ROW_BYTES;
     LCtx c;
     setup(c, &L, &cfg, &t);
-    load_learn(c, row, true);
+    load_learn(c, row);
     const int episode = c.x.episode;
     int64_t a = actions[env];
     int action = a < 0 || a > 1000 ? -1 : (int)a;
@@ -1026,7 +998,7 @@ __global__ __launch_bounds__(64) void k_learn_heuristic(const uint8_t *state, in
     if (env >= n) return;
     LCtx c;
     setup(c, &L, &cfg, &t);
-    load_learn(c, state + (size_t)env * ROW_BYTES, true);
+    load_learn(c, state + (size_t)env * ROW_BYTES);
     view_los(c);
     int a = heuristic_learn(c);
     if (c.x.lane == 0) actions[env] = a;
