@@ -29,3 +29,19 @@ def test_help_lists_the_driver_flags():
     assert r.returncode == 0
     for flag in ('--gpus', '--steps', '--warmup', '--mode', '--no-cpu-baseline'):
         assert flag in r.stdout
+
+
+def test_event_stride_samples_ten_launches():
+    """Per-kernel events in the timed region: the stride never exceeds 8 steps and always
+    leaves ten or more sampled launches of each kernel when the run has that many."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location('bench_mod', ROOT / 'bench.py')
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for steps in (1, 5, 16, 20, 37, 128, 256):
+        for per_step in (1, 2):
+            k = bench.event_stride(steps, per_step)
+            assert 1 <= k <= bench.EVERY
+            sampled = len(range(0, steps, k)) * per_step
+            assert sampled >= min(10, steps * per_step), (steps, per_step, k)
+    assert bench.event_stride(20, 2) == 4 and bench.event_stride(128, 2) == bench.EVERY
