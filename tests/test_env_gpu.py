@@ -16,6 +16,7 @@ CASES = [
     ('reference24', ('reference_config', 24), 40, 300, 19),
     ('v1_8', ('v1_config', 8), 37, 300, 9),
     ('stress40', ('stress_config',), 24, 200, 16),
+    ('crowd64', ('make_config', 64), 24, 150, 16),   # the largest layout: 41-64 monsters
 ]
 
 
