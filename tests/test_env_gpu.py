@@ -169,3 +169,31 @@ def test_level_with_an_unreachable_floor_pocket(pkg, count):
             assert not whole[tag >= 0].any(), f'step {k}: a stored field claims to reach the pocket'
             stored += int((tag >= 0).sum())
     assert dones > 0 and (count == 8 or stored > 0)
+
+
+@pytest.mark.parametrize('spec', [('baseline_config', 8), ('stress_config',)])
+def test_frozen_worlds_match_the_oracle(pkg, spec):
+    """step(actions, active=mask) with a random half of the worlds frozen each step: the
+    frozen worlds' state rows, observations and out rows stay bit for bit as they were (no
+    RNG draw, no reset), and every world equals the oracle stepped with the same mask."""
+    print(f'[parity] active mask {spec}', flush=True)
+    cfg = make(pkg, spec)
+    n = 48
+    gpu = pkg.Env(n, cfg, seed=33)
+    cpu = O.OracleEnv(n, cfg, seed=33, threads=8)
+    rng = np.random.default_rng(12)
+    frozen_steps = 0
+    for k in range(120):
+        a = rng.integers(0, 16, n).astype(np.int64) if k % 3 else cpu.heuristic()
+        on = rng.random(n) < 0.5
+        torch.cuda.synchronize()
+        before = (gpu.state.clone(), gpu.obs.clone(), gpu.out.clone())
+        cpu.step(a, active=on)
+        gpu.step(torch.from_numpy(a).to(gpu.device), active=torch.from_numpy(on).to(gpu.device))
+        torch.cuda.synchronize()
+        off = torch.from_numpy(~on).to(gpu.device)
+        for name, x, y in zip(('state', 'obs', 'out'), before, (gpu.state, gpu.obs, gpu.out)):
+            assert torch.equal(x[off], y[off]), f'step {k}: a frozen world changed its {name}'
+        frozen_steps += int((~on).sum())
+        compare(gpu, cpu, k, f'active {spec[0]}')
+    assert frozen_steps > 0
