@@ -498,7 +498,7 @@ struct Pre {
     u32x2 mon;
     uint32_t vw[4], fl[4];
     uint32_t fh;   // dword lane of the distance-field memo head (crowded layouts)
-    int64_t act;
+    int act;   // the action's low 32 bits
     int on;
 };
 __device__ __forceinline__ void prefetch_world(Pre &pf, const uint8_t *row, int max_m, const int64_t *actions,
@@ -513,7 +513,7 @@ __device__ __forceinline__ void prefetch_world(Pre &pf, const uint8_t *row, int 
         pf.fl[i] = fg[w];
     }
     pf.fh = has_fcache(max_m) ? ((const uint32_t *)(row + off_fcache(max_m)))[imin(lane, FC_HEAD - 1)] : 0u;
-    pf.act = actions[env];
+    pf.act = ((const int *)actions)[2 * (size_t)env];   // little-endian: the int64's low half
     pf.on = active ? active[env] : 1;
 }
 // load_world from the prefetched registers; RM is the config's RNG mode (a compile-time
@@ -654,13 +654,14 @@ __device__ __forceinline__ void step_worlds(Smem &sm, uint8_t *state, int n, int
         uint8_t *row = state + (size_t)env * row_bytes;
         prefetch_world(pf, row, max_m, actions, active, env, x.lane);
         const int on = __builtin_amdgcn_readfirstlane(pf.on);
-        const int64_t a = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(pf.act >> 32)) << 32 |
-                                    (uint32_t)__builtin_amdgcn_readfirstlane((int)pf.act));
+        // the int64 action's low 32 bits as a signed int, as the reference's int parameter
+        // takes it (gpu-d1/branches/d1-stairs-v2/src/learn.cu:853,904); values outside the
+        // action set are invalid actions
+        const int action = __builtin_amdgcn_readfirstlane(pf.act);
         if (!on) continue;   // an inactive env keeps its state and all its output rows
         unpack_world<RM>(x, pf, max_m);
         x.fcache = has_fcache(max_m) ? (uint32_t *)(row + off_fcache(max_m)) : nullptr;
         const uint32_t *cg = (const uint32_t *)(row + off_cells(max_m));
-        const int action = a < 0 || a > 1000 ? -1 : (int)a;
         float o8[8];
         transition(x, action, o8, cg);
         x.t++;

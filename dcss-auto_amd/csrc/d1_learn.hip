@@ -983,8 +983,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     setup(c, &L, &cfg, &t);
     load_learn(c, row);
     const int episode = c.x.episode;
-    int64_t a = actions[env];
-    int action = a < 0 || a > 1000 ? -1 : (int)a;
+    const int action = (int)actions[env];   // the low 32 bits, as the reference's int parameter
     view_los(c);
     transition_learn<CLUMP>(c, action, limit, out ? out + (size_t)env * D1L_OUT : nullptr);
     store_learn(c, row);

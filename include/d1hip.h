@@ -97,8 +97,10 @@ int d1_init(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
 
 /* Replaces learn_step / learn_step_active (gpu-d1/src/learn.cu:661-670,
  * gpu-d1/branches/d1-stairs-v2/src/learn.cu:853-875): one joint action per env
- * (int64, as the reference's trainer passes them), then the observation of the
- * post-step (post-reset when done) state. `out` is float [n, D1_OUT].
+ * (int64, as the reference's trainer passes them; its low 32 bits are the action as a
+ * signed int, as the reference's int parameter takes it, and values outside the action
+ * set are invalid actions), then the observation of the post-step (post-reset when done)
+ * state. `out` is float [n, D1_OUT].
  * `active` may be null; an inactive env keeps its state and all its output
  * rows untouched and consumes no RNG (gpu-d1/scripts/test_fast_frontier.py:89-100). */
 int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1Tables *tab,

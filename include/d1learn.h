@@ -77,7 +77,8 @@ int learn_config_bytes(void);    /* learn.cu:919 */
  * map_filter -2 gives env i map i % n_maps for its first episode. */
 int learn_init(void *state, int n, const D1LConfig *cfg, const D1LTables *tab, uint64_t seed, float *obs,
                float *mask, void *stream, int gpu);
-/* learn.cu:932-936: one joint action per env (REST repeats internal turns). */
+/* learn.cu:932-936: one joint action per env (REST repeats internal turns); an action's
+ * low 32 bits are taken as a signed int, as the reference's int parameter takes it. */
 int learn_step(void *state, int n, const D1LConfig *cfg, const D1LTables *tab, const int64_t *actions, int limit,
                float *obs, float *mask, float *out, void *stream, int gpu);
 /* learn.cu:937-941: envs with active[i] == false keep state, obs, mask and out. */

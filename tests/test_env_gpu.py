@@ -197,3 +197,22 @@ def test_frozen_worlds_match_the_oracle(pkg, spec):
         frozen_steps += int((~on).sum())
         compare(gpu, cpu, k, f'active {spec[0]}')
     assert frozen_steps > 0
+
+
+def test_out_of_range_actions_match_the_oracle(pkg):
+    """int64 actions outside the action set (negative, past 18, past 2^31, and values whose
+    low 32 bits are a valid action, as the reference's int parameter truncates them) step
+    every world exactly as the oracle does."""
+    print('[parity] out-of-range actions', flush=True)
+    cfg = pkg.baseline_config(8)
+    n = 64
+    gpu = pkg.Env(n, cfg, seed=44)
+    cpu = O.OracleEnv(n, cfg, seed=44, threads=8)
+    odd = np.array([-1, -7, 16, 17, 18, 19, 1000, 1001, 2**31 - 1, -2**31, 2**32 + 3, 2**32 + 17,
+                    2**40 + 18, -(2**33) + 5, 2**62], np.int64)
+    rng = np.random.default_rng(5)
+    for k in range(80):
+        a = np.where(rng.random(n) < 0.5, rng.choice(odd, n), rng.integers(0, 16, n)).astype(np.int64)
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, 'odd actions')

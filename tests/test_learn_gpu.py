@@ -71,8 +71,10 @@ def run_parity(L, O, floors, batch, steps, seed, clump, map_filter, check_state_
         assert np.array_equal(env.heuristic().cpu().numpy(), h), f'heuristic at step {step}'
         if rest_every and step % rest_every == 0:
             a = np.full(batch, 17, np.int64)
-        elif step % 3 == 2:   # mix in random (also invalid) actions
+        elif step % 3 == 2:   # mix in random (also invalid) actions, some past 32 bits
             a = rng.integers(-1, 21, batch).astype(np.int64)
+            wide = rng.random(batch) < 0.25   # low 32 bits an action, as the reference's int takes it
+            a[wide] += rng.choice(np.array([2**32, -(2**32), 2**40, 5 * 2**33], np.int64), int(wide.sum()))
         else:
             a = h
         env.step(torch.from_numpy(a).cuda())
