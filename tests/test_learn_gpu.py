@@ -115,6 +115,17 @@ def test_parity_rests_into_the_deadline(L, O):
     assert ref.deadline_rests > 20, ref.deadline_rests
 
 
+@pytest.mark.parametrize('limit', [1, 2])
+def test_parity_degenerate_deadlines(L, O, limit):
+    """Deadlines of one and two turns (the first or second turn of every episode reaches
+    it): each step times the episodes out and resets the worlds exactly as the CPU
+    restatement does; a deadline below one turn is refused."""
+    run_parity(L, O, [O.pkg.data.map1057()['floor']], batch=32, steps=24, seed=11, clump=0, map_filter=-1,
+               check_state_every=1, limit=limit, rest_every=3)
+    with pytest.raises(ValueError):
+        L.LearnEnv(4, limit=0)
+
+
 def test_active_mask_freezes_worlds(L, O):
     env = L.LearnEnv(32, seed=3)
     ref = O.OracleLearn(32, O.LearnTablesHost(O.pkg.data.map1057()['floor'][None]), seed=3)
