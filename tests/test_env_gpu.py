@@ -216,3 +216,26 @@ def test_out_of_range_actions_match_the_oracle(pkg):
         cpu.step(a)
         gpu.step(torch.from_numpy(a).to(gpu.device))
         compare(gpu, cpu, k, 'odd actions')
+
+
+@pytest.mark.parametrize('limit,stairs', [(3, 3), (1, 3), (5, 0)])
+def test_short_deadlines_and_stair_counts(pkg, limit, stairs):
+    """Episode deadlines of one, three and five turns (every episode times out, the worlds
+    reset every few steps), with and without stairs: state, observation, out[] and hash
+    equal the oracle's every step. Stair counts other than 0 and 3 are refused."""
+    print(f'[parity] limit {limit} stairs {stairs}', flush=True)
+    cfg = pkg.make_config(8, limit=limit, stairs=stairs, awake_pct=30)
+    n = 40
+    gpu = pkg.Env(n, cfg, seed=17)
+    cpu = O.OracleEnv(n, cfg, seed=17, threads=8)
+    rng = np.random.default_rng(21)
+    dones = 0
+    for k in range(90):
+        a = rng.integers(0, 19, n).astype(np.int64) if k % 2 else cpu.heuristic()
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, f'limit{limit}')
+        dones += int(cpu.out[:, 1].sum())
+    assert dones > 0
+    with pytest.raises(RuntimeError, match='code -2'):
+        pkg.Env(4, pkg.make_config(8, stairs=1))
