@@ -17,6 +17,7 @@ CASES = [
     ('v1_8', ('v1_config', 8), 37, 300, 9),
     ('stress40', ('stress_config',), 24, 200, 16),
     ('crowd64', ('make_config', 64), 24, 150, 16),   # the largest layout: 41-64 monsters
+    ('single', ('make_config', 1), 24, 150, 16),     # the smallest roster
 ]
 
 
