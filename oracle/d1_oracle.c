@@ -12,10 +12,13 @@
  * product never links it. Compile with -ffp-contract=off (reward arithmetic is
  * compared bit for bit).
  *
- * Parity unpinned: reset's stairs reservoir (draws from an RNG copy after the monster
- * draws), pinned by its postconditions only. The v1 reset draw order, the transition and
- * the v1 controller are pinned by the reference's own recorded v1 run
- * (gpu-d1/results/learning-v1-tests.log:1-3, tests/test_v1_reference_run.py).
+ * Parity unpinned: the values that reset's stairs reservoir draws (from an RNG copy after
+ * the monster draws): no reference log records a stairs reset. What sampling fixes about
+ * it is pinned (tests/test_reset_pins.py): it draws nothing from the play stream, its
+ * eligibility bounds are reached and never crossed, and its choice is uniform over the
+ * eligible cells. The v1 reset draw order, the transition and the v1 controller are
+ * pinned by the reference's own recorded v1 run (gpu-d1/results/learning-v1-tests.log:1-3,
+ * tests/test_v1_reference_run.py).
  */
 #include "d1_oracle.h"
 #include <stddef.h>
@@ -299,7 +302,11 @@ static int visible_awake(const OState *s, const D1Config *c) {
 
 /* Planted mistakes for the tests that show a fixture bites (0 = none, the faithful rules):
  * 1 a monster's energy drawn before its cell at reset, 2 the v1 controller's HP and
- * distance ties kept by the later candidate, 3 the player's melee damage 1 + r(5). */
+ * distance ties kept by the later candidate, 3 the player's melee damage 1 + r(5);
+ * in the stairs reservoir: 4 drawn from the play stream instead of a copy, 5 stairs more
+ * than 12 (not at least 12) from the player, 6 the spacing checked against all earlier
+ * stairs but the last, 7 the draw bound counting every cell of the list, not the
+ * eligible ones. */
 static int planted;
 void o_plant(int which) { planted = which; }
 
@@ -332,16 +339,16 @@ static void reset(OState *s, const D1Config *c) {
     }
     memset(s->viewed, 0, N);
     /* Stairs from a copy of the RNG (reservoir choice over the cell list). */
-    ORng stair = *g;
+    ORng copy = *g, *stair = planted == 4 ? g : &copy;
     s->first_stair_tick = -1;
     for (int k = 0; k < 3; k++) {
         int selected = -1, count = 0;
         if (k < c->stairs)
             for (int j = 0; j < s->ncells; j++) {
                 int p = s->cells[j];
-                int eligible = cheb(p, s->player) >= 12 && s->occ[p] < 0;
-                for (int q = 0; q < k; q++) eligible &= cheb(p, s->stairs[q]) >= 8;
-                if (eligible && rng_r(&stair, ++count) == 0) selected = p;
+                int eligible = cheb(p, s->player) >= (planted == 5 ? 13 : 12) && s->occ[p] < 0;
+                for (int q = 0; q < k - (planted == 6); q++) eligible &= cheb(p, s->stairs[q]) >= 8;
+                if (eligible && rng_r(stair, planted == 7 ? j + 1 : ++count) == 0) selected = p;
             }
         s->stairs[k] = selected;
     }

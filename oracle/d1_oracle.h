@@ -100,6 +100,7 @@ uint32_t o_hash(const OState *s, const D1Config *c);
 int o_heuristic(OState *s, const D1Config *c);
 int o_heuristic_v1(OState *s, const D1Config *c);                      /* learn.cu:599-621 */
 void o_plant(int which);   /* planted mistakes for tests (d1_oracle.c); 0 = the faithful rules */
+void lo_plant(int which);  /* the same for the learning task's reset (learn_oracle.c) */
 int o_field_offset(int k);
 void o_world_map(OState *s, const uint8_t *floor, const uint8_t *cells);
 void o_reset(OState *s, const D1Config *c);

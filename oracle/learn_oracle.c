@@ -14,10 +14,12 @@
  * agreement also checks that substitution. Compile with -ffp-contract=off.
  * Only tests/ load this; the product never links it.
  *
- * Parity unpinned (followed by reading only; no reference log or fixture fixes them):
- * lo_reset's clump anchors and stairs reservoir (draws from RNG copies; the player and
- * monster draws before them are the v1 order that the reference's recorded v1 run pins),
- * and lo_heuristic_one's priority order between its rules (each rule is pinned on its own).
+ * Parity unpinned (no reference log or fixture fixes them): the values that lo_reset's
+ * clump anchors and stairs reservoir draw from their RNG copies (the player and monster
+ * draws before them are the v1 order that the reference's recorded v1 run pins; what
+ * sampling fixes about the clumps and stairs is pinned in tests/test_reset_pins.py: no
+ * draw from the play stream, bounds reached, uniform choices), and lo_heuristic_one's
+ * priority order between its rules (each rule is pinned on its own).
  */
 #include "d1_oracle.h"
 #include "../include/d1learn.h"
@@ -207,6 +209,14 @@ int lo_nearest_stair(const LState *s, const uint16_t *ds) {
     return best;
 }
 
+/* Planted mistakes for the tests that show the reset pins bite (0 = none, the faithful
+ * rules): 1 clumps and stairs drawn from the play stream instead of copies, 2 the stairs'
+ * draw bound counting every cell of the list, not the eligible ones, 3 a clump member's
+ * draw bound counting every direction, not the free neighbours, 4 anchors needing more
+ * than two (not at least two) free neighbours. */
+static int lplanted;
+void lo_plant(int which) { lplanted = which; }
+
 /* ------------------------------------------------------------------ reset (learn.cu:351-446) */
 void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
     static const int MHP[6] = {8, 10, 12, 16, 12, 10};
@@ -228,8 +238,8 @@ void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
     }
     /* clumps of three from a copy of the RNG: a reservoir-chosen anchor with at least
      * two free floor neighbours, then two reservoir-chosen free neighbours */
-    ORng place = *g;
-    s->placement_clumped = clump == 2 || (clump == 1 && o_rng_r(&place, 3) == 0);
+    ORng place_copy = *g, *place = lplanted == 1 ? g : &place_copy;
+    s->placement_clumped = clump == 2 || (clump == 1 && o_rng_r(place, 3) == 0);
     if (s->placement_clumped) {
         for (int i = 0; i < REQ; i++) s->occ[s->pos[i]] = -1;
         for (int i = 0; i < REQ; i += 3) {
@@ -242,7 +252,7 @@ void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
                     int q = nb(p, a);
                     free_nb += floor_at(t, m, q) && q != s->player && s->occ[q] < 0;
                 }
-                if (free_nb >= 2 && o_rng_r(&place, ++eligible) == 0) anchor = p;
+                if (free_nb >= (lplanted == 4 ? 3 : 2) && o_rng_r(place, ++eligible) == 0) anchor = p;
             }
             if (anchor < 0) { s->error = 1; return; }
             s->pos[i] = (int16_t)anchor; s->occ[anchor] = (int16_t)i;
@@ -250,7 +260,9 @@ void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
                 int chosen = -1, n = 0;
                 for (int a = 0; a < 8; a++) {
                     int q = nb(anchor, a);
-                    if (floor_at(t, m, q) && q != s->player && s->occ[q] < 0 && o_rng_r(&place, ++n) == 0) chosen = q;
+                    if (floor_at(t, m, q) && q != s->player && s->occ[q] < 0 &&
+                        o_rng_r(place, lplanted == 3 ? a + 1 : ++n) == 0)
+                        chosen = q;
                 }
                 if (chosen < 0) { s->error = 1; return; }
                 s->pos[i + k] = (int16_t)chosen; s->occ[chosen] = (int16_t)(i + k);
@@ -262,7 +274,7 @@ void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
     s->frontier_count = 0;
     for (int p = 0; p < N; p++) s->frontier_slot[p] = -1;
     /* three stairs from another copy: >= 12 from the player, >= 8 from earlier stairs */
-    ORng st = *g;
+    ORng st_copy = *g, *st = lplanted == 1 ? g : &st_copy;
     s->first_stair_tick = -1;
     for (int k = 0; k < 3; k++) {
         int selected = -1, count = 0;
@@ -270,7 +282,7 @@ void lo_reset(LState *s, const D1LConfig *c, const D1LTables *t, int clump) {
             int p = cells[j];
             int ok = cheb(p, s->player) >= 12 && s->occ[p] < 0;
             for (int q = 0; q < k; q++) ok &= cheb(p, s->stairs[q]) >= 8;
-            if (ok && o_rng_r(&st, ++count) == 0) selected = p;
+            if (ok && o_rng_r(st, lplanted == 2 ? j + 1 : ++count) == 0) selected = p;
         }
         if (selected < 0) s->error = 1;
         s->stairs[k] = selected;
