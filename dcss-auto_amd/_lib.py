@@ -9,7 +9,7 @@ LIB_PATH = HERE / 'libd1hip.so'
 _LIB = None
 
 SYMBOLS = ('d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size', 'd1_config_bytes',
-           'd1_init', 'd1_step', 'd1_sample', 'd1_sample_dev', 'd1_gae', 'd1_obs_to_bf16', 'd1_obs_d4',
+           'd1_init', 'd1_step', 'd1_heuristic', 'd1_sample', 'd1_sample_dev', 'd1_gae', 'd1_obs_to_bf16', 'd1_obs_d4',
            'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step', 'd1_ppo_step_static', 'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
            'd1_sample_ar', 'd1_los_table', 'd1_distance_rows', 'd1_policy_packed_elems', 'd1_policy_pack',
            'd1_policy_fwd', 'd1_policy_fwd_sample', 'd1_policy_ar_packed_elems', 'd1_policy_ar_pack',
@@ -46,6 +46,7 @@ def load():
             getattr(L, name).argtypes = []
         L.d1_init.argtypes = [p, i, i, p, p, C.c_uint64, p, p, p]
         L.d1_step.argtypes = [p, i, i, p, p, p, p, p, p, p, p]
+        L.d1_heuristic.argtypes = [p, i, i, p, i, p, p]
         L.d1_sample.argtypes = [p, i, i, i, C.c_uint64, C.c_uint32, p, p, p]
         L.d1_sample_dev.argtypes = [p, i, i, i, C.c_uint64, p, C.c_uint32, p, p, p]
         L.d1_obs_to_bf16.argtypes = [p, p, C.c_int64, p]

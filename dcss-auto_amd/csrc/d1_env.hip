@@ -905,6 +905,120 @@ int validate(int n, int max_m, const D1Config *c, const D1Tables *t) {
     return 0;
 }
 
+// ---------------------------------------------------------------- v1 pursuit controller
+// The v1 task's scripted controller (gpu-d1/src/learn.cu:599-621, bound by
+// gpu-d1/scripts/learn_env.py:114 as heuristic()): attack the weakest adjacent living monster
+// (lowest HP, the first direction N, E, S, W, NE, SE, SW, NW among equals); otherwise take as
+// target the nearest living monster by floor distance (the lowest index among the nearest)
+// and step to the first neighbour, in direction order, that is one step closer to it; wait
+// when no living monster is reachable. Distances are 8-connected BFS layers over the world's
+// floor bitmap, as the reference's all-pairs distance rows are (learn_env.py:31-39). One
+// world per wave, lane l holding map rows l and 64 + l: the search from the player stops at
+// the first layer L that holds a living monster, the search from the target runs L - 1
+// layers, and the player's neighbours in that last layer are the ones one step closer.
+// The result is a v1 action (0-7 bump, 8 wait) or, with `joint`, this build's joint action
+// for it on the same world (a bump into a living monster's cell is ATTACK d, 8 + d; any
+// other direction MOVE d; 8 is WAIT, 16).
+__device__ __forceinline__ bool bfs_layer(Row &f0, Row &f1, Row &r0, Row &r1, const Row &fl0, const Row &fl1,
+                                          int lane) {
+    const bool has1 = lane < H - 64;
+    const Row zero{0, 0, 0};
+    const Row f0_63 = row_lane(f0, 63), f1_0 = row_lane(f1, 0);
+    const Row u0 = row_sel(lane == 0, zero, row_up(f0)), d0 = row_sel(lane == 63, f1_0, row_dn(f0));
+    const Row u1 = row_sel(lane == 0, f0_63, row_up(f1)), d1 = row_sel(lane >= H - 65, zero, row_dn(f1));
+    const Row n0 = row_andn(row_and(dilate(f0, u0, d0), fl0), r0);
+    const Row n1 = has1 ? row_andn(row_and(dilate(f1, u1, d1), fl1), r1) : zero;
+    r0 = row_or(r0, n0);
+    r1 = row_or(r1, n1);
+    f0 = n0;
+    f1 = n1;
+    return ballot(row_any(n0) || row_any(n1)) != 0;
+}
+// direction of the unit offset (dx, dy): nibble 3(dy + 1) + dx + 1 of the table
+__device__ __forceinline__ int dir_of(int dx, int dy) {
+    constexpr uint64_t T = 7ull | 0ull << 4 | 4ull << 8 | 3ull << 12 | 1ull << 20 | 6ull << 24 | 2ull << 28 | 5ull << 32;
+    return (int)((T >> (4 * (3 * (dy + 1) + dx + 1))) & 15u);
+}
+__global__ __launch_bounds__(64) void k_heuristic_v1(const uint8_t *state, int n, int max_m, size_t row_bytes,
+                                                     int count, int joint, int64_t *actions) {
+    __shared__ uint32_t bm[ROWS_WORDS];   // the living monsters' cells, later one search layer
+    const int env = blockIdx.x;           // grid = n
+    const int lane = lane_id();
+    const bool has1 = lane < H - 64;
+    const Row zero{0, 0, 0};
+    const uint8_t *row = state + (size_t)env * row_bytes;
+    const int player = ((const Hdr *)row)->player;
+    const int px = player % W, py = player / W;
+    int mpos = -1, mhp = 0;
+    if (lane < count) {
+        const Mon m = ((const Mon *)(row + OFF_MON))[lane];
+        mpos = m.pos;
+        mhp = m.hp;
+    }
+    const bool alive = lane < count && mhp > 0;
+    // the weakest adjacent living monster: HP x 8 + direction, least over the monster lanes
+    int key = 1 << 30;
+    if (alive) {
+        const int dx = mpos % W - px, dy = mpos / W - py;
+        if (iabs(dx) <= 1 && iabs(dy) <= 1) key = mhp * 8 + dir_of(dx, dy);
+    }
+    key = wave_min(key);
+    int a = 8;
+    if (key < (1 << 30)) {
+        a = key & 7;
+    } else {
+        row_st(bm, lane, zero);
+        if (has1) row_st(bm, 64 + lane, zero);
+        __syncthreads();
+        if (alive) atomicOr(&bm[(mpos / W) * RW + ((mpos % W) >> 5)], 1u << ((mpos % W) & 31));
+        __syncthreads();
+        const Row mv0 = row_ld(bm, lane), mv1 = has1 ? row_ld(bm, 64 + lane) : zero;
+        const uint32_t *fg = (const uint32_t *)(row + off_floor(max_m));
+        const Row fl0 = row_ld(fg, lane), fl1 = has1 ? row_ld(fg, 64 + lane) : zero;
+        const Row pb = row_range(px, px);
+        Row f0 = lane == py ? pb : zero, f1 = has1 && 64 + lane == py ? pb : zero;
+        Row r0 = f0, r1 = f1;
+        int L = 0;
+        bool found = false;
+        // every layer adds a cell, so the search ends within the map's cell count
+        while (bfs_layer(f0, f1, r0, r1, fl0, fl1, lane)) {
+            L++;
+            if (ballot(row_any(row_and(f0, mv0)) || row_any(row_and(f1, mv1)))) {
+                found = true;
+                break;
+            }
+        }
+        if (found) {
+            __syncthreads();
+            row_st(bm, lane, row_and(f0, mv0));
+            if (has1) row_st(bm, 64 + lane, row_and(f1, mv1));
+            __syncthreads();
+            const uint64_t hits = ballot(alive && bit(bm, mpos));
+            const int target = lane_val(mpos, __ffsll((unsigned long long)hits) - 1);
+            const int tx = target % W, ty = target / W;
+            const Row tb = row_range(tx, tx);
+            f0 = lane == ty ? tb : zero;
+            f1 = has1 && 64 + lane == ty ? tb : zero;
+            r0 = f0;
+            r1 = f1;
+            for (int k = 0; k < L - 1; k++) bfs_layer(f0, f1, r0, r1, fl0, fl1, lane);
+            __syncthreads();
+            row_st(bm, lane, f0);
+            if (has1) row_st(bm, 64 + lane, f1);
+            __syncthreads();
+            const int q = lane < 8 ? nbr(player, lane) : -1;
+            const uint64_t closer = ballot(q >= 0 && bit(bm, q));
+            if (closer) a = __ffsll((unsigned long long)closer) - 1;
+        }
+    }
+    if (joint) {
+        const int q = a < 8 ? nbr(player, a) : -1;
+        const bool bump = ballot(alive && q >= 0 && mpos == q) != 0;
+        a = a == 8 ? 16 : bump ? 8 + a : a;
+    }
+    if (lane == 0) actions[env] = a;
+}
+
 }  // namespace d1
 
 extern "C" {
@@ -961,6 +1075,17 @@ int d1_init(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
     if (n == 0) return 0;
     hipLaunchKernelGGL(d1::k_init, dim3(n), dim3(64), 0, (hipStream_t)stream, (uint8_t *)state, n, max_monsters,
                        (size_t)d1::state_bytes(max_monsters), *cfg, *tab, seed, obs, hash);
+    return (int)hipGetLastError();
+}
+int d1_heuristic(const void *state, int n, int max_monsters, const D1Config *cfg, int joint, int64_t *actions,
+                 void *stream) {
+    if (n < 0 || max_monsters < 1 || max_monsters > D1_MAX_MONSTERS || !cfg || cfg->count < 0 ||
+        cfg->count > max_monsters || (joint != 0 && joint != 1))
+        return D1_E_ARG;
+    if (!state || !actions) return D1_E_ARG;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(d1::k_heuristic_v1, dim3(n), dim3(64), 0, (hipStream_t)stream, (const uint8_t *)state, n,
+                       max_monsters, (size_t)d1::state_bytes(max_monsters), cfg->count, joint, actions);
     return (int)hipGetLastError();
 }
 int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1Tables *tab, const int64_t *actions,

@@ -120,6 +120,20 @@ class Env:
                                     self.stream), 'd1_init')
         return self.obs
 
+    def heuristic(self, v1_ids=False, out=None):
+        """The v1 pursuit controller's action for every world (d1_heuristic; the reference's
+        learn_env.py:114 heuristic(), gpu-d1/src/learn.cu:599-621), as int64 [batch]: the
+        joint actions step() takes (a bump into a living monster is ATTACK d), or with
+        `v1_ids` the v1 action ids (0-7 direction, 8 wait)."""
+        if out is None:
+            out = torch.empty(self.batch, dtype=torch.int64, device=self.device)
+        elif not (out.device == self.device and out.dtype == torch.int64 and out.is_contiguous()
+                  and out.shape == (self.batch,)):
+            raise ValueError('out must be a contiguous int64 tensor of shape [batch] on the env device')
+        _lib.check(self.lib.d1_heuristic(self.state.data_ptr(), self.batch, self.max_monsters, C.byref(self.cfg),
+                                         0 if v1_ids else 1, out.data_ptr(), self.stream), 'd1_heuristic')
+        return out
+
     def step_rows(self, lo, hi, actions):
         """Steps worlds lo..hi-1 only, with actions[lo:hi], writing their observation and
         out rows (the hash is not computed), on the current stream. Disjoint row ranges are

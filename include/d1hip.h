@@ -107,6 +107,18 @@ int d1_step(void *state, int n, int max_monsters, const D1Config *cfg, const D1T
             const int64_t *actions, uint8_t *obs, float *out, uint32_t *hash,
             const uint8_t *active, void *stream);
 
+/* Replaces learn_heuristic of the v1 library (gpu-d1/src/learn.cu:599-621,638-640,671-673;
+ * gpu-d1/scripts/learn_env.py:114, heuristic()): the v1 pursuit controller's action for
+ * each world, written to actions[n] (int64). It attacks the weakest adjacent living monster
+ * (lowest HP, then the first direction N, E, S, W, NE, SE, SW, NW), else steps to the first
+ * neighbour one floor-BFS layer closer to the nearest living monster (lowest index among
+ * the nearest), else waits. joint = 0 writes the v1 action (0-7 direction, 8 wait); joint
+ * = 1 writes the joint action d1_step takes for it on the same world (a direction into a
+ * living monster's cell is ATTACK 8 + d, another direction MOVE d, 8 is WAIT 16). The
+ * state is read only; the reference's gpu = 0 host loop has no counterpart here. */
+int d1_heuristic(const void *state, int n, int max_monsters, const D1Config *cfg, int joint,
+                 int64_t *actions, void *stream);
+
 /* ---- the reference's monster-wait benchmark workload (gpu-d1/src/bench.cu) ----
  * A stationary player at `player` on one map, `count` (<= 64) awake monsters spawned from
  * starts[fixture*64 + i], the static distance-from-player field `dist` (65535 =

@@ -15,7 +15,7 @@ def declared_symbols(header='d1hip.h', prefix='d1_'):
 
 def test_header_declares_the_abi():
     assert declared_symbols() == sorted(['d1_state_bytes', 'd1_obs_bytes', 'd1_action_size', 'd1_out_size',
-                                         'd1_config_bytes', 'd1_init', 'd1_step', 'd1_sample', 'd1_sample_dev', 'd1_gae',
+                                         'd1_config_bytes', 'd1_init', 'd1_step', 'd1_heuristic', 'd1_sample', 'd1_sample_dev', 'd1_gae',
                                          'd1_obs_to_bf16', 'd1_obs_d4', 'd1_ppo_work_bytes', 'd1_ppo_prepare', 'd1_ppo_step',
                                          'd1_ppo_step_static',
                                          'd1_wait_bytes', 'd1_wait_init', 'd1_wait_run',
@@ -80,6 +80,10 @@ def test_argument_validation_without_gpu(pkg):
     shared = pkg.reference_config()
     assert L.d1_init(1, 4, 40, C.byref(shared), C.byref(tab), 0, None, None, None) == -1  # shared map missing
     assert L.d1_step(1, 0, 8, C.byref(cfg), C.byref(tab), 1, None, None, None, None, None) == 0  # empty batch
+    assert L.d1_heuristic(1, 4, 8, C.byref(bad), 1, 1, None) == -1                  # count > capacity
+    assert L.d1_heuristic(1, 4, 8, C.byref(cfg), 2, 1, None) == -1                  # joint is 0 or 1
+    assert L.d1_heuristic(None, 4, 8, C.byref(cfg), 1, 1, None) == -1               # no state
+    assert L.d1_heuristic(1, 0, 8, C.byref(cfg), 1, 1, None) == 0                   # empty batch
 
 
 def test_ppo_step_struct_layout(tmp_path):

@@ -67,6 +67,41 @@ def test_hip_matches_oracle(pkg, name, spec, batch, steps, nact):
     print(f'[parity] {name} ok, {dones} episode ends', flush=True)
 
 
+@pytest.mark.parametrize('name,spec,batch,steps,nact', CASES)
+def test_v1_controller_matches_oracle(pkg, name, spec, batch, steps, nact):
+    """Env.heuristic (d1_heuristic, the v1 pursuit controller of gpu-d1/src/learn.cu:599-621)
+    equals the oracle's o_heuristic_v1 on every world at every step, as v1 action ids and as
+    the joint actions they stand for on each world (a bump into a living monster is ATTACK);
+    the worlds are driven by the controller's joint actions on even steps and by random
+    actions on odd ones, and stay equal to the oracle's field by field."""
+    from test_v1_reference_run import joint_actions
+    print(f'[v1 controller] {name} batch={batch}', flush=True)
+    cfg = make(pkg, spec)
+    gpu = pkg.Env(batch, cfg, seed=5)
+    cpu = O.OracleEnv(batch, cfg, seed=5, threads=8)
+    rng = np.random.default_rng(11)
+    kinds = set()
+    for k in range(min(steps, 120)):
+        v1 = cpu.heuristic_v1()
+        ids = gpu.heuristic(v1_ids=True).cpu().numpy()
+        joint = gpu.heuristic().cpu().numpy()
+        bad = np.flatnonzero(ids != v1)
+        assert not len(bad), f'{name} step {k}: world {bad[0]} v1 action gpu {ids[bad[0]]} oracle {v1[bad[0]]}'
+        f = cpu.fields()
+        want = joint_actions(f['player'], lambda i, q: f['occ'][i][q] >= 0, v1)
+        assert np.array_equal(joint, want), f'{name} step {k}: joint actions differ'
+        kinds.update(np.where(want == 16, 2, np.where(want >= 8, 1, 0)).tolist())
+        a = joint if k % 2 == 0 else rng.integers(0, nact, batch).astype(np.int64)
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, name)
+    assert {0, 1} <= kinds, f'{name}: controller cases seen {kinds}'   # moves and attacks
+    # with every monster dead the controller waits (learn.cu:613: no target)
+    for i in range(gpu.max_monsters):
+        gpu.state[:, 96 + 8 * i + 2:96 + 8 * i + 4] = 0   # Mon.hp (int16) of monster i
+    assert (gpu.heuristic(v1_ids=True) == 8).all() and (gpu.heuristic() == 16).all()
+
+
 @pytest.mark.parametrize('spec', [('baseline_config', 8), ('reference_config', 8), ('v1_config', 8),
                                   ('reference_config', 24), ('stress_config',)])
 def test_step_without_hash_is_the_same_step(pkg, spec):

@@ -2,7 +2,7 @@
 requires of its kernels: "Custom kernels must honor the stream that produces actions and
 consumes observations" (gpu-d1/scripts/test_learning.py:62-69). Each call is made once under
 the default stream and once inside `with torch.cuda.stream(side)` on tensors created there,
-and the results must be identical bit for bit: Env.step (with a reset), LearnEnv.step and
+and the results must be identical bit for bit: Env.step (with a reset) and its v1 controller, LearnEnv.step and
 its controller, the fused policy forward + sample (plain and autoregressive head), and the
 PPO minibatch step."""
 import importlib
@@ -34,13 +34,14 @@ def test_env_step_on_a_side_stream(pkg):
         g = torch.Generator(device='cuda').manual_seed(5)
         outs = []
         for k in range(40):
-            a = torch.randint(0, 19, (37,), device='cuda', generator=g)
+            # odd steps: the v1 controller's actions, made on this stream
+            a = env.heuristic() if k % 2 else torch.randint(0, 19, (37,), device='cuda', generator=g)
             env.step(a)
-            outs.append((env.obs.clone(), env.out.clone(), env.state.clone(), env.hash.clone()))
+            outs.append((env.obs.clone(), env.out.clone(), env.state.clone(), env.hash.clone(), a.clone()))
         # the reference's own case: one WAIT on fresh worlds
         env.reset(91)
         env.step(torch.full((37,), 16, dtype=torch.int64, device='cuda'))
-        outs.append((env.obs.clone(), env.out.clone(), env.state.clone(), env.hash.clone()))
+        outs.append((env.obs.clone(), env.out.clone(), env.state.clone(), env.hash.clone(), env.heuristic()))
         return outs
 
     want = run()

@@ -105,11 +105,13 @@ def test_planted_mistakes_change_the_counts(mistake):
 @pytest.mark.gpu
 @pytest.mark.parametrize('enemies', RUNS)
 def test_hip_reference_recorded_run(enemies):
-    """The same run on the HIP environment, as the reference makes it: the controller's
-    actions come from the CPU worlds and drive both (test_learning.py:48-49); each v1 action
-    is mapped on the HIP world's own decoded row. Every step the state rows (field by field),
-    the state hash, out[] and the observation must equal the oracle's, and the HIP worlds'
-    own episode ends must add up to the recorded count."""
+    """The same run on the HIP environment. The reference feeds its CPU controller's actions
+    to both simulators (test_learning.py:48-49); here the even steps take the HIP
+    controller's own actions (Env.heuristic, d1_heuristic), which must equal the CPU
+    controller's on every world (as v1 ids, and as joint actions mapped on the HIP world's
+    own decoded row), and drive both. Every step the state rows (field by field), the state
+    hash, out[] and the observation must equal the oracle's, and the HIP worlds' own
+    episode ends must add up to the recorded count."""
     import torch
     from envstate import assert_same_worlds
     print(f'[v1 run] enemies={enemies}', flush=True)
@@ -123,6 +125,11 @@ def test_hip_reference_recorded_run(enemies):
         f = gpu.fields()
         live = f['mhp'][:, :enemies] > 0
         actions = joint_actions(f['player'], lambda i, p: bool((live[i] & (f['pos'][i, :enemies] == p)).any()), v1)
+        if k % 2 == 0:   # the HIP controller's own actions drive the step
+            assert np.array_equal(gpu.heuristic(v1_ids=True).cpu().numpy(), v1), f'v1 controller at step {k}'
+            hip = gpu.heuristic().cpu().numpy()
+            assert np.array_equal(hip, actions), f'joint controller actions at step {k}'
+            actions = hip
         cpu.step(actions)
         gpu.step(torch.from_numpy(actions).cuda())
         torch.cuda.synchronize()
