@@ -18,8 +18,9 @@
  * clump anchors and stairs reservoir draw from their RNG copies (the player and monster
  * draws before them are the v1 order that the reference's recorded v1 run pins; what
  * sampling fixes about the clumps and stairs is pinned in tests/test_reset_pins.py: no
- * draw from the play stream, bounds reached, uniform choices), and lo_heuristic_one's
- * priority order between its rules (each rule is pinned on its own).
+ * draw from the play stream, bounds reached, uniform choices). lo_heuristic_one's priority
+ * order is pinned by worlds in which two of its rules apply at once
+ * (tests/test_learn_oracle.py::test_controller_priority_order).
  */
 #include "d1_oracle.h"
 #include "../include/d1learn.h"
@@ -546,21 +547,39 @@ static int explore_step(const LState *s, const D1LConfig *c, const D1LTables *t)
     }
     return -1;
 }
+/* learn.cu:881-886: the first step of the known-floor route to the nearest remembered stair,
+ * unless a visible monster holds that cell; -1 when there is none */
+static int stair_route(LState *s, const D1LTables *t, uint16_t *ds) {
+    if (!known_stairs(s)) return -1;
+    lo_known_distances(s, t, ds, 0);
+    int d = lo_route_first_step(s->player, lo_nearest_stair(s, ds), ds);
+    if (d < 0) return -1;
+    int p = nb(s->player, d);
+    return s->occ[p] >= 0 && in_view(s, t, p) ? -1 : d;
+}
+/* learn.cu:876-888, in its order: descend, attack, rest, wait, stair route, engage,
+ * explore, wait. Planted priority swaps for the tests (lplanted): 10 the attack before the
+ * descent, 11 the rest before the attack, 12 the wait before the attack, 13 the stair route
+ * before the rest, 14 the stair route before the wait, 15 the engage step before the stair
+ * route. */
 int lo_heuristic_one(LState *s, const D1LConfig *c, const D1LTables *t) {
     static __thread uint16_t ds[N];
+    const int pl = lplanted;
+    int d;
+    if (pl == 10 && (d = adjacent_attack(s, t)) >= 0) return 8 + d;
     if (stair_index(s) > 0) return 18;
-    int d = adjacent_attack(s, t);
+    const int rest = s->hp < c->hp && c->regen > 0 && !visible_awake(s, c, t);
+    if (pl == 11 && rest) return 17;
+    if (pl == 12 && visible_awake(s, c, t)) return 16;
+    d = adjacent_attack(s, t);
     if (d >= 0) return 8 + d;
-    if (s->hp < c->hp && c->regen > 0 && !visible_awake(s, c, t)) return 17;
+    if (pl == 13 && (d = stair_route(s, t, ds)) >= 0) return d;
+    if (rest) return 17;
+    if (pl == 14 && (d = stair_route(s, t, ds)) >= 0) return d;
     if (visible_awake(s, c, t)) return 16;
-    if (known_stairs(s)) {
-        lo_known_distances(s, t, ds, 0);
-        d = lo_route_first_step(s->player, lo_nearest_stair(s, ds), ds);
-        if (d >= 0) {
-            int p = nb(s->player, d);
-            if (!(s->occ[p] >= 0 && in_view(s, t, p))) return d;
-        }
-    }
+    if (pl == 15 && (d = engage_step(s, c, t)) >= 0) return d;
+    d = stair_route(s, t, ds);
+    if (d >= 0) return d;
     d = engage_step(s, c, t);
     if (d >= 0) return d;
     d = explore_step(s, c, t);

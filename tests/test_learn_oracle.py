@@ -387,3 +387,87 @@ def test_semantic_rest_sleep_deadline_invalid(O, pkg):
     s = invalid.view(O.lstate_dtype())[0]
     out = transition(O, invalid, maps, cfg, 8)
     assert out[26] == 1 and getv(s, 'ticks') == 1
+
+
+def test_controller_priority_order(O, pkg):
+    """The stairs controller's rules in the order of gpu-d1/branches/d1-stairs-v2/src/
+    learn.cu:876-888 (descend, attack the weakest adjacent visible enemy, rest, wait while an
+    awake enemy is in view, the route to a remembered stair, engage, explore): worlds on map
+    1057 in which two of them apply at once each get the earlier rule's action. Engage and
+    explore exclude each other (engage needs an enemy in view, explore none: :459,471), and
+    rest and wait do too. Each pair is shown to bite: the two rules swapped in the oracle
+    (lo_plant 10-15) change that world's action."""
+    import ctypes as C
+    maps = O.LearnTablesHost(pkg.data.map1057()['floor'][None])
+    cfg = pkg.config.learn_config()
+    L = O.learn_lib()
+    L.lo_plant.argtypes = [C.c_int]
+    L.lo_heuristic_one.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+    L.lo_route_first_step.argtypes = [C.c_int, C.c_int, C.c_void_p]
+    L.lo_nearest_stair.argtypes = [C.c_void_p, C.c_void_p]
+    t = maps.tables()
+    floor = maps.floor[:N].astype(bool)
+    DX, DY = (0, 1, 0, -1, 1, 1, -1, -1), (-1, 0, 1, 0, -1, 1, 1, -1)
+
+    def nb(p, d):
+        x, y = p % W + DX[d], p // W + DY[d]
+        return y * W + x if 0 <= x < W and 0 <= y < 70 else -1
+
+    # a floor cell whose eight neighbours are floor, and the map revealed from every cell
+    player = next(p for p in range(N) if floor[p] and all(nb(p, d) >= 0 and floor[nb(p, d)] for d in range(8)))
+    base, f = blank(O, maps)
+    for p in maps.cells[:maps.ncells[0]]:
+        setv(f, 'player', int(p))
+        L.lo_reveal(base.ctypes.data, C.byref(t))
+    setv(f, 'player', player)
+    setv(f, 'hp', cfg.hp)
+    ds = np.zeros(N, np.uint16)
+    L.lo_known_distances(base.ctypes.data, C.byref(t), ds.ctypes.data, 0)
+    stair = int(np.flatnonzero(floor & (ds < 65535))[np.argmax(ds[floor & (ds < 65535)])])   # the farthest known cell
+
+    def world(on_stair=False, hp=None, enemy=None, awake=1, known_stair=False):
+        buf = base.copy()
+        g = buf.view(O.lstate_dtype())[0]
+        if hp is not None:
+            setv(g, 'hp', hp)
+        if on_stair:
+            g['stairs'][0] = player
+        if known_stair:
+            g['stairs'][0] = stair
+            assert g['seen'][stair]
+        if enemy is not None:
+            g['pos'][0], g['mhp'][0], g['occ'][enemy], g['awake'][0], g['enemy_slot'][0] = enemy, 10, 0, awake, 0
+            g['encountered'][0] = 1
+            assert L.lo_in_view(buf.ctypes.data, C.byref(t), enemy)
+        return buf
+
+    def act(buf, plant=0):
+        L.lo_plant(plant)
+        try:
+            return L.lo_heuristic_one(buf.ctypes.data, C.byref(cfg), C.byref(t))
+        finally:
+            L.lo_plant(0)
+
+    def route(buf, goal):
+        d = np.zeros(N, np.uint16)
+        L.lo_known_distances(buf.ctypes.data, C.byref(t), d.ctypes.data, 0)
+        return L.lo_route_first_step(player, goal, d.ctypes.data)
+
+    adjacent = nb(player, 1)   # east
+    # a visible cell two or three steps away whose route's first step differs from the stair's
+    to_stair = route(world(known_stair=True), stair)
+    assert to_stair >= 0
+    far = next(p for p in range(N) if floor[p] and 2 <= max(abs(p % W - player % W), abs(p // W - player // W)) <= 3
+               and L.lo_in_view(base.ctypes.data, C.byref(t), p) and route(base, p) not in (-1, to_stair))
+    cases = [
+        # (world, faithful action, planted swap, the swapped rule's action)
+        (world(on_stair=True, enemy=adjacent), 18, 10, 8 + 1),                              # descend > attack
+        (world(hp=cfg.hp - 8, enemy=adjacent, awake=0), 8 + 1, 11, 17),                     # attack > rest
+        (world(enemy=adjacent, awake=1), 8 + 1, 12, 16),                                    # attack > wait
+        (world(hp=cfg.hp - 8, known_stair=True), 17, 13, to_stair),                         # rest > stair route
+        (world(enemy=far, awake=1, known_stair=True), 16, 14, to_stair),                    # wait > stair route
+        (world(enemy=far, awake=0, known_stair=True), to_stair, 15, route(base, far)),      # stair route > engage
+    ]
+    for k, (buf, want, plant, swapped) in enumerate(cases):
+        assert act(buf) == want, f'case {k}'
+        assert act(buf, plant) == swapped != want, f'case {k}: planted swap {plant}'
