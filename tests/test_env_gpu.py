@@ -207,6 +207,46 @@ def test_level_with_an_unreachable_floor_pocket(pkg, count):
     assert dones > 0 and (count == 8 or stored > 0)
 
 
+def test_v1_controller_with_unreachable_monsters(pkg):
+    """The pocket level with the pocket spawnable: players and monsters that start inside
+    it are walled off from the rest, so the v1 controller meets living monsters it cannot
+    reach (it waits when none is reachable, learn.cu:613, and otherwise targets the nearest
+    reachable one). Its actions equal the oracle's on every world at every step, and the
+    worlds, driven by those actions and random ones, stay equal to the oracle's."""
+    from test_v1_reference_run import joint_actions
+    print('[v1 controller] unreachable monsters', flush=True)
+    floor, cells = pocket_level(pkg)
+    cells = cells.reshape(70, 80).copy()
+    cells[7:10, 38:41] = 1
+    level = (floor, cells.reshape(-1))
+    cfg = pkg.v1_config(8, sleep=False)
+    n = 256
+    gpu = pkg.Env(n, cfg, seed=33, level=level)
+    cpu = O.OracleEnv(n, cfg, seed=33, threads=8, level=level)
+    pocket = np.zeros(5600, bool)
+    pocket.reshape(70, 80)[7:10, 38:41] = True
+    rng = np.random.default_rng(4)
+    walled_waits = split = 0
+    for k in range(60):
+        v1 = cpu.heuristic_v1()
+        ids = gpu.heuristic(v1_ids=True).cpu().numpy()
+        bad = np.flatnonzero(ids != v1)
+        assert not len(bad), f'step {k}: world {bad[0]} gpu {ids[bad[0]]} oracle {v1[bad[0]]}'
+        f = cpu.fields()
+        live = f['mhp'][:, :8] > 0
+        inside = pocket[f['pos'][:, :8].clip(0)] & live
+        player_in = pocket[f['player']]
+        walled_waits += int(((v1 == 8) & live.any(1) & (player_in != inside.any(1))).sum())
+        split += int((live.any(1) & (inside.any(1) != player_in)).sum())
+        joint = joint_actions(f['player'], lambda i, q: f['occ'][i][q] >= 0, v1)
+        assert np.array_equal(gpu.heuristic().cpu().numpy(), joint), f'step {k}: joint actions differ'
+        a = joint if k % 2 == 0 else rng.integers(0, 19, n).astype(np.int64)
+        cpu.step(a)
+        gpu.step(torch.from_numpy(a).to(gpu.device))
+        compare(gpu, cpu, k, 'unreachable')
+    assert walled_waits > 0 and split > 0, (walled_waits, split)
+
+
 @pytest.mark.parametrize('spec', [('baseline_config', 8), ('stress_config',)])
 def test_frozen_worlds_match_the_oracle(pkg, spec):
     """step(actions, active=mask) with a random half of the worlds frozen each step: the
