@@ -339,6 +339,40 @@ def stress_bench(args, envs=262144, horizon=256, warmup=4):
             'roofline': roofline('d1::k_step', achieved, step_ms, STEP_BYTES[40], traffic, len(events))}
 
 
+def controller_bench(args, warmup=8):
+    """The v1 task (map 1057, 8 monsters, all awake) at --envs worlds driven by the v1 pursuit
+    controller on the GPU (Env.heuristic -> d1_heuristic, gpu-d1/src/learn.cu:599-621) then
+    the env step, --steps timed decisions; HIP events time each kernel."""
+    import torch
+    pkg = importlib.import_module('dcss-auto_amd')
+    n = args.envs
+    env = pkg.Env(n, pkg.v1_config(8, sleep=False), seed=1, hash=False)
+    actions = torch.zeros(n, dtype=torch.int64, device='cuda')
+    for _ in range(warmup):
+        env.step(env.heuristic(out=actions))
+    torch.cuda.synchronize()
+    every = event_stride(args.steps)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, every)]
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        ev = events[k // every] if k % every == 0 else None
+        if ev is not None:
+            ev[0].record()
+        env.heuristic(out=actions)
+        if ev is not None:
+            ev[1].record()
+        env.step(actions)
+        if ev is not None:
+            ev[2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ctl_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
+    step_ms = sum(e[1].elapsed_time(e[2]) for e in events) / len(events)
+    return {'metric': 'v1 controller + env step decisions/sec', 'value': n * args.steps / wall, 'unit': 'decisions/s',
+            'envs': n, 'steps': args.steps, 'controller_ms': ctl_ms, 'step_ms': step_ms,
+            'config': {'workload': 'v1 task, map 1057, 8 awake monsters', 'controller': 'd1_heuristic (joint actions)'}}
+
+
 # Algorithmic bytes of one learning-task decision (k_learn_step): fp32 observation 4060 +
 # mask 76 + outcome 180 + action 8 + 2 x (80 header + 192 enemies) + 2 x 840 memory
 # bitmap + 840 floor bitmap; the frontier list (2 bytes per anchor read, changed
@@ -413,7 +447,7 @@ def main():
     ap.add_argument('--monsters', type=int, default=8)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--mode', choices=['rollout', 'counters', 'ppo', 'train', 'panel', 'wait', 'stress',
-                                       'stress-counters', 'learn'],
+                                       'stress-counters', 'learn', 'controller'],
                     default='rollout',
                     help='counters: a 256 MiB copy (counter calibration) then env steps only, for rocprofv3 --pmc; '
                          'stress-counters: the same calibration, then the C5 stress workload untimed; '
@@ -444,6 +478,9 @@ def main():
         return
     if args.mode == 'learn':
         print(json.dumps(learn_bench(args)), flush=True)
+        return
+    if args.mode == 'controller':
+        print(json.dumps(controller_bench(args)), flush=True)
         return
     if args.mode == 'panel':
         print(json.dumps(panel_bench(args)), flush=True)
