@@ -315,3 +315,75 @@ def test_short_deadlines_and_stair_counts(pkg, limit, stairs):
     assert dones > 0
     with pytest.raises(RuntimeError, match='code -2'):
         pkg.Env(4, pkg.make_config(8, stairs=1))
+
+
+def test_v1_controller_ties(pkg):
+    """The v1 controller's tie-breaks, from the reference's rules (gpu-d1/src/learn.cu:599-621)
+    on worlds edited in the HIP state rows: among equally weak adjacent monsters the first
+    direction (N, E, S, W, NE, SE, SW, NW) is attacked, a weaker one wins over an earlier
+    direction; among equally near monsters (floor BFS) the lowest index is the target, and
+    the step is the first neighbour one layer closer to it."""
+    print('[v1 controller] ties', flush=True)
+    DX, DY = (0, 1, 0, -1, 1, 1, -1, -1), (-1, 0, 1, 0, -1, 1, 1, -1)
+    cfg = pkg.v1_config(8, sleep=False)
+    env = pkg.Env(64, cfg, seed=12)
+    f = env.fields()
+    floor = env.floors()[0].astype(bool)
+    mon = 96   # Mon rows: pos, hp (int16), energy (int16), awake, kind
+
+    def nb(p, d):
+        x, y = p % 80 + DX[d], p // 80 + DY[d]
+        return y * 80 + x if 0 <= x < 80 and 0 <= y < 70 else -1
+
+    def bfs(src):
+        dist = np.full(5600, 65535, np.int64)
+        dist[src] = 0
+        frontier = [src]
+        while frontier:
+            nxt = []
+            for p in frontier:
+                for d in range(8):
+                    q = nb(p, d)
+                    if q >= 0 and floor[q] and dist[q] == 65535:
+                        dist[q] = dist[p] + 1
+                        nxt.append(q)
+            frontier = nxt
+        return dist
+
+    def place(w, cells_hp):
+        """monsters 0.. on the given cells with the given HP; the rest dead"""
+        for i in range(8):
+            pos, hp = cells_hp[i] if i < len(cells_hp) else (0, 0)
+            raw = np.array([pos, hp], np.int16).view(np.uint8)
+            env.state[w, mon + 8 * i:mon + 8 * i + 4] = torch.from_numpy(raw.copy()).to(env.device)
+
+    checked = 0
+    for w in range(64):
+        p = int(f['player'][w])
+        free = [d for d in range(8) if nb(p, d) >= 0 and floor[nb(p, d)]]
+        if len(free) < 2:
+            continue
+        da, db = free[0], free[-1]
+        place(w, [(nb(p, db), 5), (nb(p, da), 5)])        # equal HP: the earlier direction
+        assert int(env.heuristic(v1_ids=True)[w]) == da
+        assert int(env.heuristic()[w]) == 8 + da
+        place(w, [(nb(p, db), 4), (nb(p, da), 5)])        # weaker wins over the earlier direction
+        assert int(env.heuristic(v1_ids=True)[w]) == db
+        # two monsters at the same floor distance >= 3 in different places: the lower index is the target
+        dist = bfs(p)
+        for k in (3, 4, 5):
+            ring = np.flatnonzero(dist == k)
+            if len(ring) < 2:
+                continue
+            a, b = int(ring[-1]), int(ring[0])
+            back = bfs(a)
+            want = next(d for d in range(8) if nb(p, d) >= 0 and floor[nb(p, d)] and back[nb(p, d)] == k - 1)
+            place(w, [(a, 9), (b, 9)])
+            assert int(env.heuristic(v1_ids=True)[w]) == want, (w, k)
+            back_b = bfs(b)
+            want_b = next(d for d in range(8) if nb(p, d) >= 0 and floor[nb(p, d)] and back_b[nb(p, d)] == k - 1)
+            place(w, [(b, 9), (a, 9)])
+            assert int(env.heuristic(v1_ids=True)[w]) == want_b, (w, k)
+            checked += 1
+            break
+    assert checked >= 16, checked
